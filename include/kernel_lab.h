@@ -1,0 +1,127 @@
+/*
+ * kernel_lab C-ABI: fused residual-add + RMSNorm and paged-KV decode attention
+ * for AMD Instinct MI355X (gfx950).
+ *
+ * The header is plain C. It includes no HIP, PyTorch or C++ header, so any
+ * FFI (ctypes, cgo, JNI, a C++ serving loop) can bind it directly. Every
+ * pointer is a device pointer unless stated otherwise; every launch is
+ * asynchronous on `stream` and never synchronises the host.
+ *
+ * Reference interface replaced: `kernel_lab::launch_rms_norm` and
+ * `kernel_lab::launch_paged_decode_attention` in csrc/kernel_lab.h:17-33 of
+ * Markkoby3/Kernel-lab, plus the split-KV contract of
+ * kernel_lab/triton_kernels/paged_attention.py:169-264 (num_splits,
+ * max_seq_len, fp32 partials).
+ */
+#ifndef KERNEL_LAB_H_
+#define KERNEL_LAB_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Same handle type as HIP's hipStream_t, declared without including HIP. */
+typedef struct ihipStream_t* kl_stream_t;
+
+/* Element types. Replaces `enum class DType` (csrc/kernel_lab.h:12). */
+typedef enum kl_dtype {
+  KL_DTYPE_F32 = 0,
+  KL_DTYPE_F16 = 1,
+  KL_DTYPE_BF16 = 2
+} kl_dtype;
+
+/*
+ * Status codes. The reference launchers return cudaError_t and signal
+ * unsupported shapes with cudaErrorInvalidValue (csrc/paged_attention.cu:157,
+ * 174, 198); here argument errors and runtime errors are told apart.
+ */
+typedef enum kl_status {
+  KL_OK = 0,
+  KL_ERR_INVALID_ARGUMENT = 1, /* bad pointer, size, dtype or stride        */
+  KL_ERR_UNSUPPORTED = 2,      /* a shape this build has no kernel for      */
+  KL_ERR_WORKSPACE = 3,        /* workspace missing or smaller than needed  */
+  KL_ERR_HIP = 4               /* the HIP runtime reported an error         */
+} kl_status;
+
+/* Static text for a status code. */
+const char* kl_status_string(int status);
+
+/*
+ * Detail of the last failed call on the calling thread (argument name,
+ * HIP error text), or "" if the last call succeeded. Valid until the next
+ * kernel_lab call on this thread.
+ */
+const char* kl_last_error(void);
+
+/* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
+int kl_version(void);
+
+/*
+ * RMSNorm over `rows` rows of length `hidden`.
+ * Replaces kernel_lab::launch_rms_norm (csrc/kernel_lab.h:14-19).
+ *
+ *   residual == NULL:  out = rmsnorm(x) * weight
+ *   residual != NULL:  residual = dtype(f32(x) + f32(residual))   (in place)
+ *                      out      = rmsnorm(residual) * weight
+ *
+ * `out`, `residual` and `weight` are contiguous; row i of `x` starts at
+ * x + i * x_row_stride elements (x_row_stride >= hidden). rows == 0 is a
+ * successful no-op. Math is fp32; `out` is rounded to nearest even.
+ */
+int kl_rms_norm(kl_dtype dtype, void* out, const void* x, void* residual, const void* weight,
+                int64_t rows, int64_t hidden, int64_t x_row_stride, float eps,
+                kl_stream_t stream);
+
+/*
+ * Split planning for paged decode. Pure host arithmetic: it reads no device
+ * memory (in particular not seq_lens), so it never synchronises.
+ * Follows choose_num_splits and the split normalisation of
+ * kernel_lab/triton_kernels/paged_attention.py:169-173,205-211, with the
+ * workgroup target sized for the device's compute units.
+ *
+ *   max_pages        block-table columns any sequence may use
+ *                    (= cdiv(max_seq_len, page_size) when that is known)
+ *   num_splits       requested KV splits; 0 lets the planner choose
+ *   cu_count         compute units to plan for; 0 queries the current device
+ *   out_num_splits   (host pointer) splits the launch will use
+ *   out_workspace    (host pointer) bytes of device workspace the launch needs
+ *                    (0 when the launch needs none)
+ */
+int kl_paged_decode_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads,
+                         int head_dim, int page_size, int max_pages, int num_splits,
+                         int cu_count, int* out_num_splits, size_t* out_workspace);
+
+/*
+ * Single-token decode attention over a paged KV cache (NHD layout).
+ * Replaces kernel_lab::launch_paged_decode_attention (csrc/kernel_lab.h:21-33)
+ * and the split-KV wrapper of kernel_lab/triton_kernels/paged_attention.py:176-264.
+ *
+ *   q, out        [batch, num_q_heads, head_dim]                    contiguous
+ *   k/v_cache     [num_pages, page_size, num_kv_heads, head_dim]    contiguous
+ *   block_table   [batch, block_table_stride] int32 page ids
+ *   seq_lens      [batch] int32, each in [1, max_pages * page_size]
+ *
+ * Sequence b attends over its first seq_lens[b] cached tokens, following
+ * block_table[b, 0 .. cdiv(seq_lens[b], page_size)). Entries past that and
+ * pages not named there are never read. num_q_heads must be a multiple of
+ * num_kv_heads (grouped-query attention). `scale` multiplies q.k.
+ * num_splits == 0 lets the planner choose. The workspace must hold at least
+ * the bytes kl_paged_decode_plan reports for the same arguments; it may be
+ * NULL when that is 0. batch == 0 is a successful no-op.
+ */
+int kl_paged_decode_attention(kl_dtype dtype, void* out, const void* q, const void* k_cache,
+                              const void* v_cache, const int32_t* block_table,
+                              const int32_t* seq_lens, int batch, int num_q_heads,
+                              int num_kv_heads, int head_dim, int page_size,
+                              int64_t block_table_stride, int max_pages, float scale,
+                              int num_splits, void* workspace, size_t workspace_bytes,
+                              kl_stream_t stream);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* KERNEL_LAB_H_ */

@@ -1,0 +1,127 @@
+// Device helpers shared by the gfx950 kernels: element conversions with
+// round-to-nearest-even, 16-byte vector types, and wave64 reductions built on
+// DPP row operations plus lane reads.
+//
+// Reference counterpart: csrc/common.cuh:11-66 (Num<T>, Pack<T,N>, warp_sum,
+// block_sum). The reference reduces over 32-lane warps with xor shuffles; on
+// CDNA a wavefront has 64 lanes, so the reductions here work within DPP rows
+// of 16 lanes and then combine the four rows.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kl {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------- elements
+// Element traits. `S` is the storage type in memory; to_f32/from_f32 are the
+// exact widening and the round-to-nearest-even narrowing that PyTorch's
+// `.float()` and `.to(dtype)` perform.
+struct F32 {
+  using S = float;
+  static constexpr int kBytes = 4;
+  static __device__ __forceinline__ float to_f32(S v) { return v; }
+  static __device__ __forceinline__ S from_f32(float f) { return f; }
+};
+
+struct F16 {
+  using S = uint16_t;
+  static constexpr int kBytes = 2;
+  static __device__ __forceinline__ float to_f32(S v) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, v));
+  }
+  // v_cvt_f16_f32 rounds to nearest even in the default float mode.
+  static __device__ __forceinline__ S from_f32(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+  }
+};
+
+struct BF16 {
+  using S = uint16_t;
+  static constexpr int kBytes = 2;
+  static __device__ __forceinline__ float to_f32(S v) {
+    return __builtin_bit_cast(float, static_cast<uint32_t>(v) << 16);
+  }
+  // gfx950 converts with v_cvt_pk_bf16_f32, round to nearest even.
+  static __device__ __forceinline__ S from_f32(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+  }
+};
+
+// Low / high 16-bit halves of a 32-bit word as floats (fp16 or bf16 storage).
+template <typename E>
+__device__ __forceinline__ float lo_f32(uint32_t w) {
+  return E::to_f32(static_cast<uint16_t>(w & 0xffffu));
+}
+template <typename E>
+__device__ __forceinline__ float hi_f32(uint32_t w) {
+  return E::to_f32(static_cast<uint16_t>(w >> 16));
+}
+
+// Two floats rounded to 16-bit and packed, first in the low half.
+template <typename E>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  return static_cast<uint32_t>(E::from_f32(a)) | (static_cast<uint32_t>(E::from_f32(b)) << 16);
+}
+
+// ------------------------------------------------------------------- DPP
+// dpp_ctrl encodings (GCN3+ DPP): quad_perm is two bits per lane of a quad;
+// row_ror:n rotates the 16 lanes of each row by n.
+constexpr int kDppQuadSwap1 = 0xB1;  // quad_perm [1,0,3,2]: lane ^ 1
+constexpr int kDppQuadSwap2 = 0x4E;  // quad_perm [2,3,0,1]: lane ^ 2
+constexpr int kDppRowRor4 = 0x124;
+constexpr int kDppRowRor8 = 0x128;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float lane_read(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Sum over the 16 lanes of each DPP row; every lane of the row gets its row's sum.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp<kDppQuadSwap1>(v);
+  v += dpp<kDppQuadSwap2>(v);
+  v += dpp<kDppRowRor4>(v);
+  v += dpp<kDppRowRor8>(v);
+  return v;
+}
+
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp<kDppQuadSwap1>(v));
+  v = fmaxf(v, dpp<kDppQuadSwap2>(v));
+  v = fmaxf(v, dpp<kDppRowRor4>(v));
+  v = fmaxf(v, dpp<kDppRowRor8>(v));
+  return v;
+}
+
+// Sum over the whole wave64, returned wave-uniform. The four row sums are
+// added in a fixed order, so the result does not depend on scheduling.
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  return (lane_read(v, 0) + lane_read(v, 16)) + (lane_read(v, 32) + lane_read(v, 48));
+}
+
+// Cross-row exchange (lane ^ 16, lane ^ 32) through the LDS crossbar.
+__device__ __forceinline__ float shfl_xor(float v, int mask) {
+  const int lane = __lane_id();
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ mask) << 2,
+                                                                __builtin_bit_cast(int, v)));
+}
+
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+}  // namespace kl

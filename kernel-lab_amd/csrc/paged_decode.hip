@@ -1,0 +1,874 @@
+// Paged-KV decode attention for gfx950: split-KV flash-decoding with GQA
+// packing and an exact base-2 log-sum-exp merge.
+//
+// Behavioural spec: kernel_lab/triton_kernels/paged_attention.py:37-264
+// (split kernel, merge kernel, split planner) and kernel_lab/reference.py:33-68
+// (the math). Drop-in boundary: csrc/paged_attention.cu:180-199 and
+// csrc/kernel_lab.h:21-33.
+//
+// Work unit: (sequence b, KV head, head group, split). A split owns a range of
+// `pages_per_split` pages of its sequence. Its workgroup has four waves; the
+// unit's 16-token blocks go round-robin to the waves, each wave keeps its own
+// running max / normaliser / output, and the waves merge through LDS at the
+// end. With one split the workgroup writes the final output; otherwise it
+// writes an fp32 partial output and its log2-sum-exp, and a merge kernel
+// combines the splits of each (sequence, query head).
+//
+// MFMA path (fp16 / bf16, page_size % 16 == 0, head_dim in {32,64,128,256}):
+//   S  = K . Q^T    v_mfma_f32_16x16x32_{f16,bf16}: rows = 16 tokens of a
+//                   block, columns = up to 16 query heads of the GQA group.
+//                   K goes from HBM straight into the A operand (lane = token,
+//                   8 consecutive head dims per lane, 16-byte loads).
+//   O^T += V^T P^T  v_mfma_f32_16x16x16_{f16,bf16}: the score tile's output
+//                   layout (lane = head, 4 consecutive tokens) is exactly the
+//                   B operand layout, so P never leaves registers. V is loaded
+//                   with fully coalesced 16-byte loads, staged in a per-wave
+//                   LDS tile and read back transposed as the A operand.
+// Every K/V element is read from HBM once per unit and used by the whole GQA
+// group. Tokens past seq_len inside the last page are excluded by selects
+// (scores to -inf, V rows to zero), never by multiplying by zero, so NaN or
+// garbage there cannot leak; pages past cdiv(seq_len, page_size) and pages not
+// named by the block table are never read.
+//
+// VALU path (fp32, and shapes the MFMA path does not take): lanes own 16-byte
+// slices of a token's head dims; dot products reduce across the lanes of a
+// token; each lane keeps an online softmax per query head and lanes merge by
+// the log-sum-exp rule at the end.
+#include <algorithm>
+#include <cmath>
+#include <type_traits>
+
+#include "hip_common.h"
+#include "kl_internal.h"
+
+namespace kl {
+namespace {
+
+constexpr int kWaves = 4;      // waves per workgroup
+constexpr int kThreads = kWaves * 64;
+constexpr int kBlock = 16;     // tokens per MFMA block
+constexpr int kMaxPlannedSplits = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct DecodeArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* out;
+  const int32_t* block_table;
+  const int32_t* seq_lens;
+  float* o_part;    // [batch, num_q_heads, num_splits, head_dim]
+  float* lse_part;  // [batch, num_q_heads, num_splits], log2 domain
+  int64_t bt_stride;
+  int64_t page_stride;  // elements between pages: page_size * num_kv_heads * head_dim
+  int token_stride;     // elements between tokens of a page: num_kv_heads * head_dim
+  int batch;
+  int num_q_heads;
+  int num_kv_heads;
+  int group;            // num_q_heads / num_kv_heads
+  int page_size;
+  int max_pages;
+  int num_splits;
+  int pages_per_split;
+  int head_groups;      // workgroups per (sequence, KV head, split) along the group
+  int heads_per_wg;     // query heads one workgroup handles
+  float scale_log2;     // scale * log2(e)
+};
+
+struct Unit {
+  int b, kvh, hg, split;
+  int seq_len;          // clamped to max_pages * page_size
+  int page_begin, page_end;
+};
+
+__device__ __forceinline__ Unit decode_unit(const DecodeArgs& a) {
+  Unit u;
+  int idx = blockIdx.x;
+  u.split = idx % a.num_splits;
+  idx /= a.num_splits;
+  u.hg = idx % a.head_groups;
+  idx /= a.head_groups;
+  u.kvh = idx % a.num_kv_heads;
+  u.b = idx / a.num_kv_heads;
+  const int raw = a.seq_lens[u.b];
+  const int64_t cap = static_cast<int64_t>(a.max_pages) * a.page_size;
+  u.seq_len = static_cast<int>(raw < cap ? raw : cap);
+  const int num_pages = u.seq_len > 0 ? (u.seq_len + a.page_size - 1) / a.page_size : 0;
+  u.page_begin = u.split * a.pages_per_split;
+  u.page_end = min(u.page_begin + a.pages_per_split, num_pages);
+  return u;
+}
+
+// Writes zeros for the heads of an empty sequence (seq_len <= 0). The math of
+// kernel_lab/reference.py:58-67 gives zeros there (softmax over no tokens, then
+// an empty weighted sum).
+template <typename E>
+__device__ void write_zero_heads(const DecodeArgs& a, const Unit& u, int head_dim) {
+  using S = typename E::S;
+  const int h0 = u.hg * a.heads_per_wg;
+  const int nh = min(a.heads_per_wg, a.group - h0);
+  S* out = static_cast<S*>(a.out);
+  for (int i = threadIdx.x; i < nh * head_dim; i += blockDim.x) {
+    const int h = u.kvh * a.group + h0 + i / head_dim;
+    out[(static_cast<int64_t>(u.b) * a.num_q_heads + h) * head_dim + i % head_dim] = E::from_f32(0.0f);
+  }
+}
+
+// ------------------------------------------------------------ MFMA split path
+
+template <typename E>
+struct Mfma;
+
+template <>
+struct Mfma<F16> {
+  static __device__ __forceinline__ f32x4 qk(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                  0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 pv(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c, 0,
+                                                 0, 0);
+  }
+};
+
+template <>
+struct Mfma<BF16> {
+  static __device__ __forceinline__ f32x4 qk(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                   c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 pv(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4, a),
+                                                     __builtin_bit_cast(bf16x4, b), c, 0, 0, 0);
+  }
+};
+
+// LDS bytes the MFMA kernel needs: the per-wave V staging tiles during the
+// main loop, reused for the cross-wave merge afterwards.
+template <int D, int NT>
+struct MfmaLds {
+  static constexpr int kVRow = D + 4;  // elements per staged token row (pad spreads banks)
+  static constexpr int kStageBytes = kWaves * kBlock * kVRow * 2;
+  static constexpr int kAccBytes = (kWaves - 1) * NT * (D / 16) * 4 * 64 * 4;
+  static constexpr int kMlBytes = kWaves * NT * 16 * 2 * 4;
+  static constexpr int kBytes =
+      kStageBytes > kAccBytes + kMlBytes ? kStageBytes : kAccBytes + kMlBytes;
+};
+
+template <typename E, int D, int NT>
+__global__ void __launch_bounds__(kThreads) decode_mfma_kernel(const DecodeArgs a) {
+  using S = typename E::S;
+  using M = Mfma<E>;
+  constexpr int KC = D / 32;           // QK k-chunks; also 16-byte K and V loads per lane per block
+  constexpr int DT = D / 16;           // PV output tiles along head_dim
+  constexpr int LPT = D / 8;           // lanes per token row in the V load
+  constexpr int TPL = 64 / LPT;        // tokens per V load instruction
+  constexpr int VROW = MfmaLds<D, NT>::kVRow;
+  __shared__ __attribute__((aligned(16))) char lds[MfmaLds<D, NT>::kBytes];
+
+  const Unit u = decode_unit(a);
+  if (u.page_begin >= u.page_end) {
+    if (u.split == 0 && u.seq_len <= 0 && a.num_splits == 1) write_zero_heads<E>(a, u, D);
+    return;  // a split past the end of its sequence has no work
+  }
+
+  const int lane = __lane_id();
+  const int wave = wave_id();
+  const int row = lane & 15;  // MFMA row / column index of this lane
+  const int grp = lane >> 4;  // MFMA k-group of this lane
+  const int h0 = u.hg * a.heads_per_wg;
+
+  // Q as the B operand of S = K Q^T: lane holds head (h0 + 16t + row), dims
+  // 32c + 8grp .. +7 for chunk c. Heads past the group are zero.
+  u32x4 qf[NT][KC];
+  {
+    const S* q = static_cast<const S*>(a.q);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int hl = h0 + 16 * t + row;
+      const bool valid = hl < a.group;
+      const S* qh = q + (static_cast<int64_t>(u.b) * a.num_q_heads + u.kvh * a.group + (valid ? hl : 0)) * D;
+#pragma unroll
+      for (int c = 0; c < KC; ++c) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(qh + 32 * c + 8 * grp);
+        qf[t][c] = valid ? v : u32x4{0, 0, 0, 0};
+      }
+    }
+  }
+
+  float m[NT], l[NT];
+  f32x4 acc[NT][DT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    m[t] = -INFINITY;
+    l[t] = 0.0f;
+#pragma unroll
+    for (int d = 0; d < DT; ++d) acc[t][d] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+
+  const S* kc = static_cast<const S*>(a.k);
+  const S* vc = static_cast<const S*>(a.v);
+  const int32_t* bt = a.block_table + static_cast<int64_t>(u.b) * a.bt_stride;
+  const int bpp = a.page_size / kBlock;  // blocks per page
+  const int blk_begin = u.page_begin * bpp;
+  const int blk_end = min(u.page_end * bpp, (u.seq_len + kBlock - 1) / kBlock);
+  // This wave's blocks: blk_begin + wave + kWaves * i, i < nblk.
+  const int first = blk_begin + wave;
+  const int nblk = first < blk_end ? (blk_end - first + kWaves - 1) / kWaves : 0;
+
+  // Per-lane element offsets inside a block (token row x head dims).
+  const int k_off = row * a.token_stride + 8 * grp;
+  const int v_tok = lane / LPT;
+  const int v_dim = 8 * (lane % LPT);
+  const int v_off = v_tok * a.token_stride + v_dim;
+  S* stage = reinterpret_cast<S*>(lds) + wave * kBlock * VROW;
+
+  auto load_block = [&](int blk, u32x4 (&kf)[KC], u32x4 (&vf)[KC]) {
+    const int64_t page = bt[blk / bpp];
+    const int64_t base = page * a.page_stride + static_cast<int64_t>((blk % bpp) * kBlock) * a.token_stride +
+                         static_cast<int64_t>(u.kvh) * D;
+    const S* kb = kc + base;
+    const S* vb = vc + base;
+#pragma unroll
+    for (int c = 0; c < KC; ++c) kf[c] = *reinterpret_cast<const u32x4*>(kb + k_off + 32 * c);
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+      vf[c] = *reinterpret_cast<const u32x4*>(vb + v_off + static_cast<int64_t>(c * TPL) * a.token_stride);
+    }
+  };
+
+  auto process_block = [&](int blk, const u32x4 (&kf)[KC], const u32x4 (&vf)[KC]) {
+    const int nvalid = u.seq_len - blk * kBlock;  // >= 1; >= 16 means all valid
+
+    // Stage V (rows past seq_len as zeros) for the transposed reads below.
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+      const int tok = c * TPL + v_tok;
+      const u32x4 v = tok < nvalid ? vf[c] : u32x4{0, 0, 0, 0};
+      u32x2* dst = reinterpret_cast<u32x2*>(stage + tok * VROW + v_dim);
+      dst[0] = u32x2{v[0], v[1]};
+      dst[1] = u32x2{v[2], v[3]};
+    }
+
+    // Scores: lane holds S[token 4grp + i][head row] for tile t.
+    u32x2 pf[NT];
+    float alpha[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int c = 0; c < KC; ++c) s = M::qk(kf[c], qf[t][c], s);
+      float sc[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sc[i] = (4 * grp + i < nvalid) ? s[i] * a.scale_log2 : -INFINITY;
+      float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+      mx = fmaxf(mx, shfl_xor(mx, 16));
+      mx = fmaxf(mx, shfl_xor(mx, 32));
+      // Token 0 of every processed block is valid, so mx and m_new are finite.
+      const float m_new = fmaxf(m[t], mx);
+      alpha[t] = exp2f(m[t] - m_new);
+      float p[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p[i] = exp2f(sc[i] - m_new);
+      l[t] = l[t] * alpha[t] + ((p[0] + p[1]) + (p[2] + p[3]));
+      m[t] = m_new;
+      pf[t] = u32x2{pack2<E>(p[0], p[1]), pack2<E>(p[2], p[3])};
+    }
+
+    // V^T as the A operand: lane holds V[token 4grp + j][dim 16dt + row].
+    const S* src = stage + (4 * grp) * VROW + row;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const uint32_t v0 = src[0 * VROW + 16 * dt];
+      const uint32_t v1 = src[1 * VROW + 16 * dt];
+      const uint32_t v2 = src[2 * VROW + 16 * dt];
+      const uint32_t v3 = src[3 * VROW + 16 * dt];
+      const u32x2 va = {v0 | (v1 << 16), v2 | (v3 << 16)};
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        acc[t][dt] *= alpha[t];
+        acc[t][dt] = M::pv(va, pf[t], acc[t][dt]);
+      }
+    }
+  };
+
+  if (nblk > 0) {
+    u32x4 k0[KC], v0[KC], k1[KC], v1[KC];
+    load_block(first, k0, v0);
+    int i = 0;
+    while (true) {
+      if (i + 1 < nblk) {
+        load_block(first + (i + 1) * kWaves, k1, v1);
+        process_block(first + i * kWaves, k0, v0);
+      } else {
+        process_block(first + i * kWaves, k0, v0);
+        break;
+      }
+      ++i;
+      if (i + 1 < nblk) {
+        load_block(first + (i + 1) * kWaves, k0, v0);
+        process_block(first + i * kWaves, k1, v1);
+      } else {
+        process_block(first + i * kWaves, k1, v1);
+        break;
+      }
+      ++i;
+    }
+  }
+
+  // Per-wave normaliser: the four lane groups hold disjoint tokens of a head.
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    l[t] += shfl_xor(l[t], 16);
+    l[t] += shfl_xor(l[t], 32);
+  }
+
+  // Cross-wave merge. The LDS staging tiles are reused, so wait for every wave
+  // to leave the main loop first.
+  __syncthreads();
+  float* lds_acc = reinterpret_cast<float*>(lds);
+  float* lds_ml = lds_acc + (kWaves - 1) * NT * DT * 4 * 64;
+  if (lane < 16) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      lds_ml[((wave * NT + t) * 16 + lane) * 2 + 0] = m[t];
+      lds_ml[((wave * NT + t) * 16 + lane) * 2 + 1] = l[t];
+    }
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          lds_acc[((((wave - 1) * NT + t) * DT + dt) * 4 + i) * 64 + lane] = acc[t][dt][i];
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (wave != 0) return;
+
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    float mw[kWaves], lw[kWaves];
+    float mmax = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      mw[w] = lds_ml[((w * NT + t) * 16 + row) * 2 + 0];
+      lw[w] = lds_ml[((w * NT + t) * 16 + row) * 2 + 1];
+      mmax = fmaxf(mmax, mw[w]);
+    }
+    float cw[kWaves];
+    float denom = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      cw[w] = mw[w] == -INFINITY ? 0.0f : exp2f(mw[w] - mmax);
+      denom += lw[w] * cw[w];
+    }
+    const int hl = h0 + 16 * t + row;
+    const bool valid = hl < a.group;
+    const int64_t head = static_cast<int64_t>(u.b) * a.num_q_heads + u.kvh * a.group + hl;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      float o[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float num = acc[t][dt][i] * cw[0];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) {
+          num += lds_acc[((((w - 1) * NT + t) * DT + dt) * 4 + i) * 64 + lane] * cw[w];
+        }
+        o[i] = num / denom;
+      }
+      if (!valid) continue;
+      const int d = 16 * dt + 4 * grp;
+      if (a.num_splits == 1) {
+        S* out = static_cast<S*>(a.out) + head * D + d;
+        *reinterpret_cast<u32x2*>(out) = u32x2{pack2<E>(o[0], o[1]), pack2<E>(o[2], o[3])};
+      } else {
+        float* op = a.o_part + (head * a.num_splits + u.split) * D + d;
+        *reinterpret_cast<f32x4*>(op) = f32x4{o[0], o[1], o[2], o[3]};
+      }
+    }
+    if (valid && a.num_splits > 1 && grp == 0) {
+      a.lse_part[head * a.num_splits + u.split] = mmax + log2f(denom);
+    }
+  }
+}
+
+// ------------------------------------------------------------ VALU split path
+
+// The elements of a 16-byte slice as floats.
+template <typename E>
+__device__ __forceinline__ void unpack16(u32x4 v, float (&f)[16 / E::kBytes]) {
+  if constexpr (E::kBytes == 4) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f[i] = __builtin_bit_cast(float, v[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = lo_f32<E>(v[i]);
+      f[2 * i + 1] = hi_f32<E>(v[i]);
+    }
+  }
+}
+
+template <int TPT>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int mask = 1; mask < TPT; mask <<= 1) v += shfl_xor(v, mask);
+  return v;
+}
+
+template <typename E, int D, int GMAX>
+struct ValuCfg {
+  static constexpr int kVec = 16 / E::kBytes;                     // elements per 16-byte slice
+  static constexpr int kTpt = D / kVec;                           // lanes per token
+  static constexpr int kTpw = 64 / kTpt;                          // tokens per wave step
+  static constexpr int kLdsFloats = kWaves * GMAX * (D + 2);
+};
+
+template <typename E, int D, int GMAX>
+__global__ void __launch_bounds__(kThreads) decode_valu_kernel(const DecodeArgs a) {
+  using S = typename E::S;
+  using C = ValuCfg<E, D, GMAX>;
+  constexpr int VEC = C::kVec;
+  constexpr int TPT = C::kTpt;
+  constexpr int TPW = C::kTpw;
+  static_assert(TPT >= 1 && TPT <= 64 && (TPT & (TPT - 1)) == 0, "head_dim slices must tile a wave");
+  __shared__ float lds[C::kLdsFloats];
+
+  const Unit u = decode_unit(a);
+  if (u.page_begin >= u.page_end) {
+    if (u.split == 0 && u.seq_len <= 0 && a.num_splits == 1) write_zero_heads<E>(a, u, D);
+    return;
+  }
+  const int lane = __lane_id();
+  const int wave = wave_id();
+  const int slot = lane / TPT;
+  const int dv = (lane % TPT) * VEC;
+  const int h0 = u.hg * a.heads_per_wg;
+  const int nh = min(GMAX, a.group - h0);
+
+  float qv[GMAX][VEC];
+  {
+    const S* q = static_cast<const S*>(a.q);
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+      const int hl = g < nh ? h0 + g : h0;
+      const S* qh = q + (static_cast<int64_t>(u.b) * a.num_q_heads + u.kvh * a.group + hl) * D + dv;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) qv[g][e] = g < nh ? E::to_f32(qh[e]) : 0.0f;
+    }
+  }
+
+  float m[GMAX], l[GMAX], acc[GMAX][VEC];
+#pragma unroll
+  for (int g = 0; g < GMAX; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[g][e] = 0.0f;
+  }
+
+  const S* kc = static_cast<const S*>(a.k);
+  const S* vc = static_cast<const S*>(a.v);
+  const int32_t* bt = a.block_table + static_cast<int64_t>(u.b) * a.bt_stride;
+  const int tok_begin = u.page_begin * a.page_size;
+  const int tok_end = min(u.page_end * a.page_size, u.seq_len);
+  const int steps = (tok_end - tok_begin + kWaves * TPW - 1) / (kWaves * TPW);
+
+  for (int it = 0; it < steps; ++it) {
+    const int tok = tok_begin + it * kWaves * TPW + wave * TPW + slot;
+    const bool valid = tok < tok_end;
+    u32x4 kx = {0, 0, 0, 0}, vx = {0, 0, 0, 0};
+    if (valid) {
+      const int64_t page = bt[tok / a.page_size];
+      const int64_t off = page * a.page_stride + static_cast<int64_t>(tok % a.page_size) * a.token_stride +
+                          static_cast<int64_t>(u.kvh) * D + dv;
+      kx = *reinterpret_cast<const u32x4*>(kc + off);
+      vx = *reinterpret_cast<const u32x4*>(vc + off);
+    }
+    float kf[VEC], vf[VEC];
+    unpack16<E>(kx, kf);
+    unpack16<E>(vx, vf);
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+      float dot = 0.0f;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) dot += qv[g][e] * kf[e];
+      const float s = group_sum<TPT>(dot) * a.scale_log2;
+      if (valid) {
+        const float m_new = fmaxf(m[g], s);
+        const float alpha = exp2f(m[g] - m_new);
+        const float p = exp2f(s - m_new);
+        l[g] = l[g] * alpha + p;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[g][e] = acc[g][e] * alpha + p * vf[e];
+        m[g] = m_new;
+      }
+    }
+  }
+
+  // Merge the token slots of this wave (lanes with equal dims), log-sum-exp rule.
+#pragma unroll
+  for (int mask = TPT; mask < 64; mask <<= 1) {
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+      const float mo = shfl_xor(m[g], mask);
+      const float lo = shfl_xor(l[g], mask);
+      const float mm = fmaxf(m[g], mo);
+      const float c0 = m[g] == -INFINITY ? 0.0f : exp2f(m[g] - mm);
+      const float c1 = mo == -INFINITY ? 0.0f : exp2f(mo - mm);
+      l[g] = l[g] * c0 + lo * c1;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float ao = shfl_xor(acc[g][e], mask);
+        acc[g][e] = acc[g][e] * c0 + ao * c1;
+      }
+      m[g] = mm;
+    }
+  }
+
+  // Merge the waves through LDS; wave 0 writes.
+  float* wl = lds + wave * GMAX * (D + 2);
+  if (slot == 0) {
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) wl[g * (D + 2) + dv + e] = acc[g][e];
+      if (dv == 0) {
+        wl[g * (D + 2) + D] = m[g];
+        wl[g * (D + 2) + D + 1] = l[g];
+      }
+    }
+  }
+  __syncthreads();
+  if (wave != 0 || slot != 0) return;
+#pragma unroll
+  for (int g = 0; g < GMAX; ++g) {
+    if (g >= nh) break;
+    float mw[kWaves], mmax = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      mw[w] = lds[(w * GMAX + g) * (D + 2) + D];
+      mmax = fmaxf(mmax, mw[w]);
+    }
+    float cw[kWaves], denom = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      cw[w] = mw[w] == -INFINITY ? 0.0f : exp2f(mw[w] - mmax);
+      denom += lds[(w * GMAX + g) * (D + 2) + D + 1] * cw[w];
+    }
+    const int64_t head = static_cast<int64_t>(u.b) * a.num_q_heads + u.kvh * a.group + h0 + g;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      float num = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) num += lds[(w * GMAX + g) * (D + 2) + dv + e] * cw[w];
+      const float o = num / denom;
+      if (a.num_splits == 1) {
+        static_cast<S*>(a.out)[head * D + dv + e] = E::from_f32(o);
+      } else {
+        a.o_part[(head * a.num_splits + u.split) * D + dv + e] = o;
+      }
+    }
+    if (a.num_splits > 1 && dv == 0) a.lse_part[head * a.num_splits + u.split] = mmax + log2f(denom);
+  }
+}
+
+// --------------------------------------------------------------- split merge
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = row16_max(v);
+  return fmaxf(fmaxf(lane_read(v, 0), lane_read(v, 16)), fmaxf(lane_read(v, 32), lane_read(v, 48)));
+}
+
+// out[b, h] = sum_s 2^(lse_s - M) o_s / sum_s 2^(lse_s - M) over the splits that
+// hold tokens of sequence b (kernel_lab/triton_kernels/paged_attention.py:134-166).
+// Splits past the end of a sequence are never read, so their workspace may hold
+// anything.
+template <typename E>
+__global__ void __launch_bounds__(64) decode_merge_kernel(const DecodeArgs a, int head_dim) {
+  using S = typename E::S;
+  const int bh = blockIdx.x;
+  const int b = bh / a.num_q_heads;
+  const int lane = __lane_id();
+  const int raw = a.seq_lens[b];
+  const int64_t cap = static_cast<int64_t>(a.max_pages) * a.page_size;
+  const int seq_len = static_cast<int>(raw < cap ? raw : cap);
+  const int num_pages = seq_len > 0 ? (seq_len + a.page_size - 1) / a.page_size : 0;
+  const int active = min(a.num_splits, (num_pages + a.pages_per_split - 1) / a.pages_per_split);
+  S* out = static_cast<S*>(a.out) + static_cast<int64_t>(bh) * head_dim;
+  if (active <= 0) {
+    for (int d = lane; d < head_dim; d += 64) out[d] = E::from_f32(0.0f);
+    return;
+  }
+  const float* lse = a.lse_part + static_cast<int64_t>(bh) * a.num_splits;
+  const float* op = a.o_part + static_cast<int64_t>(bh) * a.num_splits * head_dim;
+
+  float mx = -INFINITY;
+  for (int s = lane; s < active; s += 64) mx = fmaxf(mx, lse[s]);
+  mx = wave_max(mx);
+  float den = 0.0f;
+  for (int s = lane; s < active; s += 64) den += exp2f(lse[s] - mx);
+  den = wave_sum(den);
+
+  for (int d = lane; d < head_dim; d += 64) {
+    float num = 0.0f;
+    for (int s = 0; s < active; ++s) num += exp2f(lse[s] - mx) * op[static_cast<int64_t>(s) * head_dim + d];
+    out[d] = E::from_f32(num / den);
+  }
+}
+
+// -------------------------------------------------------------- host side
+
+bool mfma_path(kl_dtype dtype, int head_dim, int page_size) {
+  return (dtype == KL_DTYPE_F16 || dtype == KL_DTYPE_BF16) && page_size % kBlock == 0 &&
+         (head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256);
+}
+
+bool valu_head_dim_ok(kl_dtype dtype, int head_dim) {
+  const int vec = dtype == KL_DTYPE_F32 ? 4 : 8;
+  switch (head_dim) {
+    case 16:
+    case 32:
+    case 64:
+    case 128:
+    case 256:
+      return head_dim / vec <= 64 && head_dim >= vec;
+    default:
+      return false;
+  }
+}
+
+// Query heads one workgroup takes from a GQA group, and the resulting number of
+// workgroups per (sequence, KV head, split).
+void head_tiling(kl_dtype dtype, int head_dim, int page_size, int group, int* per_wg, int* groups) {
+  int cap;
+  if (mfma_path(dtype, head_dim, page_size)) {
+    cap = (group > 16 && head_dim <= 128) ? 32 : 16;
+  } else {
+    cap = 8;
+  }
+  int per = std::min(group, cap);
+  if (!mfma_path(dtype, head_dim, page_size)) {
+    per = per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : 8;  // template sizes of the VALU kernel
+  }
+  *per_wg = per;
+  *groups = static_cast<int>(cdiv(group, per));
+}
+
+struct Plan {
+  int num_splits;
+  int pages_per_split;
+  int heads_per_wg;
+  int head_groups;
+  size_t o_bytes;
+  size_t ws_bytes;
+};
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t n) { return (n + kAlign - 1) / kAlign * kAlign; }
+
+int make_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads, int head_dim, int page_size,
+              int max_pages, int num_splits, int cu_count, Plan* p) {
+  if (batch < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 || max_pages < 0) {
+    return fail(KL_ERR_INVALID_ARGUMENT, "batch, heads, head_dim, page_size and max_pages must be positive");
+  }
+  if (num_q_heads % num_kv_heads != 0) {
+    return fail(KL_ERR_INVALID_ARGUMENT, "num_q_heads must be a multiple of num_kv_heads");
+  }
+  if (num_splits < 0) return fail(KL_ERR_INVALID_ARGUMENT, "num_splits must be >= 0");
+  if (dtype != KL_DTYPE_F32 && dtype != KL_DTYPE_F16 && dtype != KL_DTYPE_BF16) {
+    return fail(KL_ERR_UNSUPPORTED, "dtype must be f32, f16 or bf16");
+  }
+  if (!mfma_path(dtype, head_dim, page_size) && !valu_head_dim_ok(dtype, head_dim)) {
+    return fail(KL_ERR_UNSUPPORTED, "head_dim must be 16, 32, 64, 128 or 256");
+  }
+  const int group = num_q_heads / num_kv_heads;
+  head_tiling(dtype, head_dim, page_size, group, &p->heads_per_wg, &p->head_groups);
+  const int pages = std::max(max_pages, 1);
+  int s = num_splits;
+  if (s == 0) {
+    // About two workgroups per compute unit, never more splits than pages
+    // (choose_num_splits, kernel_lab/triton_kernels/paged_attention.py:169-173).
+    const int cus = cu_count > 0 ? cu_count : 256;
+    const int64_t units = std::max<int64_t>(1, static_cast<int64_t>(batch) * num_kv_heads * p->head_groups);
+    const int64_t wanted = cdiv(2LL * cus, units);
+    s = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>({wanted, pages, kMaxPlannedSplits})));
+  }
+  // Normalise: drop splits no sequence can reach (paged_attention.py:210-211).
+  const int pps = static_cast<int>(cdiv(pages, s));
+  s = static_cast<int>(cdiv(pages, pps));
+  p->num_splits = s;
+  p->pages_per_split = pps;
+  if (s > 1) {
+    const size_t rows = static_cast<size_t>(batch) * num_q_heads * s;
+    p->o_bytes = align_up(rows * head_dim * sizeof(float));
+    p->ws_bytes = p->o_bytes + align_up(rows * sizeof(float));
+  } else {
+    p->o_bytes = 0;
+    p->ws_bytes = 0;
+  }
+  return ok();
+}
+
+template <typename E>
+int launch_split(const DecodeArgs& a, int head_dim, bool mfma, unsigned grid, hipStream_t stream) {
+  if (mfma) {
+    if constexpr (!std::is_same_v<E, F32>) {
+      const bool two = a.heads_per_wg > 16;
+      switch (head_dim) {
+        case 32:
+          two ? decode_mfma_kernel<E, 32, 2><<<grid, kThreads, 0, stream>>>(a)
+              : decode_mfma_kernel<E, 32, 1><<<grid, kThreads, 0, stream>>>(a);
+          return KL_OK;
+        case 64:
+          two ? decode_mfma_kernel<E, 64, 2><<<grid, kThreads, 0, stream>>>(a)
+              : decode_mfma_kernel<E, 64, 1><<<grid, kThreads, 0, stream>>>(a);
+          return KL_OK;
+        case 128:
+          two ? decode_mfma_kernel<E, 128, 2><<<grid, kThreads, 0, stream>>>(a)
+              : decode_mfma_kernel<E, 128, 1><<<grid, kThreads, 0, stream>>>(a);
+          return KL_OK;
+        case 256:
+          decode_mfma_kernel<E, 256, 1><<<grid, kThreads, 0, stream>>>(a);
+          return KL_OK;
+      }
+    }
+    return fail(KL_ERR_UNSUPPORTED, "no MFMA kernel for this head_dim");
+  }
+#define KL_VALU_CASE(DIM)                                                                     \
+  case DIM:                                                                                   \
+    if constexpr (DIM / (16 / E::kBytes) >= 1 && DIM / (16 / E::kBytes) <= 64) {              \
+      switch (a.heads_per_wg) {                                                               \
+        case 1:                                                                               \
+          decode_valu_kernel<E, DIM, 1><<<grid, kThreads, 0, stream>>>(a);                    \
+          return KL_OK;                                                                       \
+        case 2:                                                                               \
+          decode_valu_kernel<E, DIM, 2><<<grid, kThreads, 0, stream>>>(a);                    \
+          return KL_OK;                                                                       \
+        case 4:                                                                               \
+          decode_valu_kernel<E, DIM, 4><<<grid, kThreads, 0, stream>>>(a);                    \
+          return KL_OK;                                                                       \
+        default:                                                                              \
+          decode_valu_kernel<E, DIM, 8><<<grid, kThreads, 0, stream>>>(a);                    \
+          return KL_OK;                                                                       \
+      }                                                                                       \
+    }                                                                                         \
+    break;
+  switch (head_dim) {
+    KL_VALU_CASE(16)
+    KL_VALU_CASE(32)
+    KL_VALU_CASE(64)
+    KL_VALU_CASE(128)
+    KL_VALU_CASE(256)
+  }
+#undef KL_VALU_CASE
+  return fail(KL_ERR_UNSUPPORTED, "no kernel for this head_dim");
+}
+
+template <typename E>
+int launch_typed(DecodeArgs& a, int head_dim, bool mfma, hipStream_t stream) {
+  const int64_t wgs = static_cast<int64_t>(a.batch) * a.num_kv_heads * a.head_groups * a.num_splits;
+  if (wgs > 0x7fffffffLL) return fail(KL_ERR_UNSUPPORTED, "too many workgroups");
+  int st = launch_split<E>(a, head_dim, mfma, static_cast<unsigned>(wgs), stream);
+  if (st != KL_OK) return st;
+  st = check_launch("paged decode split kernel launch");
+  if (st != KL_OK) return st;
+  if (a.num_splits > 1) {
+    decode_merge_kernel<E><<<static_cast<unsigned>(static_cast<int64_t>(a.batch) * a.num_q_heads), 64, 0, stream>>>(
+        a, head_dim);
+    st = check_launch("paged decode merge kernel launch");
+  }
+  return st;
+}
+
+}  // namespace
+}  // namespace kl
+
+extern "C" int kl_paged_decode_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                    int page_size, int max_pages, int num_splits, int cu_count,
+                                    int* out_num_splits, size_t* out_workspace) {
+  using namespace kl;
+  if (cu_count <= 0) cu_count = current_cu_count();
+  Plan p;
+  const int st =
+      make_plan(dtype, batch, num_q_heads, num_kv_heads, head_dim, page_size, max_pages, num_splits, cu_count, &p);
+  if (st != KL_OK) return st;
+  if (out_num_splits) *out_num_splits = p.num_splits;
+  if (out_workspace) *out_workspace = p.ws_bytes;
+  return ok();
+}
+
+extern "C" int kl_paged_decode_attention(kl_dtype dtype, void* out, const void* q, const void* k_cache,
+                                         const void* v_cache, const int32_t* block_table, const int32_t* seq_lens,
+                                         int batch, int num_q_heads, int num_kv_heads, int head_dim, int page_size,
+                                         int64_t block_table_stride, int max_pages, float scale, int num_splits,
+                                         void* workspace, size_t workspace_bytes, kl_stream_t stream) {
+  using namespace kl;
+  if (batch == 0) return ok();
+  Plan p;
+  int st = make_plan(dtype, batch, num_q_heads, num_kv_heads, head_dim, page_size, max_pages, num_splits,
+                     current_cu_count(), &p);
+  if (st != KL_OK) return st;
+  if (!out || !q || !k_cache || !v_cache || !block_table || !seq_lens) {
+    return fail(KL_ERR_INVALID_ARGUMENT, "out, q, k_cache, v_cache, block_table and seq_lens must be non-null");
+  }
+  if (max_pages < 1) return fail(KL_ERR_INVALID_ARGUMENT, "max_pages must be >= 1");
+  if (block_table_stride < max_pages && batch > 1) {
+    return fail(KL_ERR_INVALID_ARGUMENT, "block_table_stride must be >= max_pages");
+  }
+  const uintptr_t align_mask = 15;
+  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache) |
+       reinterpret_cast<uintptr_t>(out)) & align_mask) {
+    return fail(KL_ERR_INVALID_ARGUMENT, "q, out and the caches must be 16-byte aligned");
+  }
+  if (p.ws_bytes > 0 && (workspace == nullptr || workspace_bytes < p.ws_bytes)) {
+    return fail(KL_ERR_WORKSPACE, "workspace smaller than kl_paged_decode_plan reported");
+  }
+  if ((reinterpret_cast<uintptr_t>(workspace) & align_mask) != 0) {
+    return fail(KL_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+  }
+
+  DecodeArgs a;
+  a.q = q;
+  a.k = k_cache;
+  a.v = v_cache;
+  a.out = out;
+  a.block_table = block_table;
+  a.seq_lens = seq_lens;
+  a.o_part = static_cast<float*>(workspace);
+  a.lse_part = workspace ? reinterpret_cast<float*>(static_cast<char*>(workspace) + p.o_bytes) : nullptr;
+  a.bt_stride = block_table_stride;
+  a.page_stride = static_cast<int64_t>(page_size) * num_kv_heads * head_dim;
+  const int64_t token_stride = static_cast<int64_t>(num_kv_heads) * head_dim;
+  if (token_stride > 0x7fffffffLL / 64) return fail(KL_ERR_UNSUPPORTED, "num_kv_heads * head_dim too large");
+  a.token_stride = static_cast<int>(token_stride);
+  a.batch = batch;
+  a.num_q_heads = num_q_heads;
+  a.num_kv_heads = num_kv_heads;
+  a.group = num_q_heads / num_kv_heads;
+  a.page_size = page_size;
+  a.max_pages = max_pages;
+  a.num_splits = p.num_splits;
+  a.pages_per_split = p.pages_per_split;
+  a.head_groups = p.head_groups;
+  a.heads_per_wg = p.heads_per_wg;
+  a.scale_log2 = scale * kLog2e;
+
+  const bool mfma = mfma_path(dtype, head_dim, page_size);
+  const auto s = reinterpret_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case KL_DTYPE_F32:
+      return launch_typed<F32>(a, head_dim, false, s);
+    case KL_DTYPE_F16:
+      return launch_typed<F16>(a, head_dim, mfma, s);
+    case KL_DTYPE_BF16:
+      return launch_typed<BF16>(a, head_dim, mfma, s);
+  }
+  return fail(KL_ERR_UNSUPPORTED, "dtype must be f32, f16 or bf16");
+}

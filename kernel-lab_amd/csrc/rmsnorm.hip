@@ -1,0 +1,245 @@
+// RMSNorm and fused residual-add + RMSNorm for gfx950.
+//
+// Math (reference: csrc/rmsnorm.cu:17-62 and kernel_lab/reference.py:13-30):
+//   res = dtype(f32(x) + f32(res))                  (fused variant only)
+//   rstd = 1 / sqrt(sum(f32(res)^2) / hidden + eps)
+//   out = dtype((f32(res) * rstd) * f32(weight))
+// The sum is rounded to the storage dtype before it is normalised, because
+// that rounded value is what the residual stream keeps; the residual output is
+// therefore bit-identical to PyTorch's.
+//
+// Design: one workgroup per row. Each thread loads its share of the row as
+// 16-byte packs, strided by the workgroup size so every wave load is one
+// contiguous 1 KiB span, and keeps the values in registers. The sum of squares
+// is reduced within each wave by DPP, across waves through LDS with one
+// barrier, and the output is written from registers: one read of x and the
+// residual, one write of the residual and the output, nothing re-read.
+// Rows too wide for the register budget use a two-pass variant whose second
+// pass re-reads the row.
+#include <algorithm>
+
+#include "hip_common.h"
+#include "kl_internal.h"
+
+namespace kl {
+namespace {
+
+template <typename S, int N>
+struct alignas(sizeof(S) * N) Pack {
+  S v[N];
+};
+
+constexpr int kMaxThreads = 1024;
+
+// Workgroup-wide sum; every thread receives the same value. `scratch` holds one
+// float per wave. Wave sums are added in wave order, so the result is
+// deterministic.
+__device__ __forceinline__ float block_sum(float v, float* scratch) {
+  const float w = wave_sum(v);
+  const int nw = blockDim.x >> 6;
+  if (__lane_id() == 0) scratch[threadIdx.x >> 6] = w;
+  __syncthreads();
+  float total = 0.0f;
+  for (int i = 0; i < nw; ++i) total += scratch[i];
+  return total;
+}
+
+__device__ __forceinline__ float inv_rms(float sum_sq, int hidden, float eps) {
+  // Division and square root are IEEE-rounded here (no fast-math), matching
+  // torch.rsqrt on the CPU, which computes 1 / sqrt(x).
+  return 1.0f / sqrtf(sum_sq / static_cast<float>(hidden) + eps);
+}
+
+// Register-resident single pass. Thread t owns packs t, t + NT, ..., so NPACK
+// loads per tensor per thread; NT * NPACK * VEC >= hidden.
+template <typename E, int VEC, int NPACK, bool HAS_RES>
+__global__ void __launch_bounds__(kMaxThreads)
+    rms_norm_reg_kernel(typename E::S* __restrict__ out, const typename E::S* __restrict__ x,
+                        typename E::S* __restrict__ res, const typename E::S* __restrict__ weight,
+                        int hidden, int64_t x_row_stride, float eps) {
+  using S = typename E::S;
+  using P = Pack<S, VEC>;
+  __shared__ float scratch[kMaxThreads / 64];
+
+  const int64_t row = blockIdx.x;
+  const int packs = hidden / VEC;
+  const int nt = blockDim.x;
+  const P* xr = reinterpret_cast<const P*>(x + row * x_row_stride);
+  P* rr = HAS_RES ? reinterpret_cast<P*>(res + row * static_cast<int64_t>(hidden)) : nullptr;
+  P* orow = reinterpret_cast<P*>(out + row * static_cast<int64_t>(hidden));
+  const P* wr = reinterpret_cast<const P*>(weight);
+
+  P a[NPACK];
+  P b[NPACK];
+#pragma unroll
+  for (int k = 0; k < NPACK; ++k) {
+    const int p = threadIdx.x + k * nt;
+    if (p < packs) {
+      a[k] = xr[p];
+      if constexpr (HAS_RES) b[k] = rr[p];
+    }
+  }
+
+  float f[NPACK][VEC];
+  float sum_sq = 0.0f;
+#pragma unroll
+  for (int k = 0; k < NPACK; ++k) {
+    const int p = threadIdx.x + k * nt;
+    if (p < packs) {
+      if constexpr (HAS_RES) {
+        P s;
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) s.v[j] = E::from_f32(E::to_f32(a[k].v[j]) + E::to_f32(b[k].v[j]));
+        rr[p] = s;
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) f[k][j] = E::to_f32(s.v[j]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) f[k][j] = E::to_f32(a[k].v[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) sum_sq += f[k][j] * f[k][j];
+    }
+  }
+
+  // Weights are loaded before the barrier so their latency overlaps it.
+  P w[NPACK];
+#pragma unroll
+  for (int k = 0; k < NPACK; ++k) {
+    const int p = threadIdx.x + k * nt;
+    if (p < packs) w[k] = wr[p];
+  }
+
+  const float rstd = inv_rms(block_sum(sum_sq, scratch), hidden, eps);
+
+#pragma unroll
+  for (int k = 0; k < NPACK; ++k) {
+    const int p = threadIdx.x + k * nt;
+    if (p < packs) {
+      P o;
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) o.v[j] = E::from_f32((f[k][j] * rstd) * E::to_f32(w[k].v[j]));
+      orow[p] = o;
+    }
+  }
+}
+
+// Two-pass variant for rows wider than the register-resident kernel takes.
+// Pass 1 writes the residual and reduces; pass 2 re-reads the row the same
+// thread wrote (no cross-thread dependency, so no extra barrier).
+template <typename E, int VEC, bool HAS_RES>
+__global__ void __launch_bounds__(kMaxThreads)
+    rms_norm_stream_kernel(typename E::S* __restrict__ out, const typename E::S* __restrict__ x,
+                           typename E::S* __restrict__ res, const typename E::S* __restrict__ weight,
+                           int hidden, int64_t x_row_stride, float eps) {
+  using S = typename E::S;
+  using P = Pack<S, VEC>;
+  __shared__ float scratch[kMaxThreads / 64];
+
+  const int64_t row = blockIdx.x;
+  const int packs = hidden / VEC;
+  const P* xr = reinterpret_cast<const P*>(x + row * x_row_stride);
+  P* rr = HAS_RES ? reinterpret_cast<P*>(res + row * static_cast<int64_t>(hidden)) : nullptr;
+  P* orow = reinterpret_cast<P*>(out + row * static_cast<int64_t>(hidden));
+  const P* wr = reinterpret_cast<const P*>(weight);
+
+  float sum_sq = 0.0f;
+  for (int p = threadIdx.x; p < packs; p += blockDim.x) {
+    P a = xr[p];
+    if constexpr (HAS_RES) {
+      const P r = rr[p];
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) a.v[j] = E::from_f32(E::to_f32(a.v[j]) + E::to_f32(r.v[j]));
+      rr[p] = a;
+    }
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      const float f = E::to_f32(a.v[j]);
+      sum_sq += f * f;
+    }
+  }
+  const float rstd = inv_rms(block_sum(sum_sq, scratch), hidden, eps);
+
+  const P* src = HAS_RES ? rr : xr;
+  for (int p = threadIdx.x; p < packs; p += blockDim.x) {
+    const P a = src[p];
+    const P g = wr[p];
+    P o;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) o.v[j] = E::from_f32((E::to_f32(a.v[j]) * rstd) * E::to_f32(g.v[j]));
+    orow[p] = o;
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <typename E, int VEC, bool HAS_RES>
+int launch_vec(void* out, const void* x, void* res, const void* w, int64_t rows, int hidden,
+               int64_t x_row_stride, float eps, hipStream_t stream) {
+  using S = typename E::S;
+  auto* o = static_cast<S*>(out);
+  auto* xi = static_cast<const S*>(x);
+  auto* r = static_cast<S*>(res);
+  auto* wi = static_cast<const S*>(w);
+  const int packs = hidden / VEC;
+  // About four packs per thread, in whole waves, 64..1024 threads.
+  int threads = static_cast<int>(std::min<int64_t>(kMaxThreads, std::max<int64_t>(64, cdiv(cdiv(packs, 4), 64) * 64)));
+  const int npack = static_cast<int>(cdiv(packs, threads));
+  const dim3 grid(static_cast<unsigned>(rows));
+  if (npack <= 1) {
+    rms_norm_reg_kernel<E, VEC, 1, HAS_RES><<<grid, threads, 0, stream>>>(o, xi, r, wi, hidden, x_row_stride, eps);
+  } else if (npack <= 2) {
+    rms_norm_reg_kernel<E, VEC, 2, HAS_RES><<<grid, threads, 0, stream>>>(o, xi, r, wi, hidden, x_row_stride, eps);
+  } else if (npack <= 4) {
+    rms_norm_reg_kernel<E, VEC, 4, HAS_RES><<<grid, threads, 0, stream>>>(o, xi, r, wi, hidden, x_row_stride, eps);
+  } else if (npack <= 8) {
+    rms_norm_reg_kernel<E, VEC, 8, HAS_RES><<<grid, threads, 0, stream>>>(o, xi, r, wi, hidden, x_row_stride, eps);
+  } else {
+    rms_norm_stream_kernel<E, VEC, HAS_RES><<<grid, kMaxThreads, 0, stream>>>(o, xi, r, wi, hidden, x_row_stride, eps);
+  }
+  return check_launch("rms_norm kernel launch");
+}
+
+template <typename E>
+int launch_typed(void* out, const void* x, void* res, const void* w, int64_t rows, int hidden,
+                 int64_t x_row_stride, float eps, hipStream_t stream) {
+  constexpr int kVec = 16 / E::kBytes;
+  const bool vec = hidden % kVec == 0 && x_row_stride % kVec == 0 && aligned16(out) && aligned16(x) &&
+                   aligned16(w) && (res == nullptr || aligned16(res));
+  if (vec) {
+    return res ? launch_vec<E, kVec, true>(out, x, res, w, rows, hidden, x_row_stride, eps, stream)
+               : launch_vec<E, kVec, false>(out, x, res, w, rows, hidden, x_row_stride, eps, stream);
+  }
+  return res ? launch_vec<E, 1, true>(out, x, res, w, rows, hidden, x_row_stride, eps, stream)
+             : launch_vec<E, 1, false>(out, x, res, w, rows, hidden, x_row_stride, eps, stream);
+}
+
+}  // namespace
+}  // namespace kl
+
+extern "C" int kl_rms_norm(kl_dtype dtype, void* out, const void* x, void* residual, const void* weight,
+                           int64_t rows, int64_t hidden, int64_t x_row_stride, float eps,
+                           kl_stream_t stream) {
+  using namespace kl;
+  if (rows < 0 || hidden < 0) return fail(KL_ERR_INVALID_ARGUMENT, "rows and hidden must be >= 0");
+  if (rows == 0 || hidden == 0) return ok();
+  if (rows > 0x7fffffffLL) return fail(KL_ERR_UNSUPPORTED, "rows must be < 2^31");
+  if (hidden > 0x7fffffffLL) return fail(KL_ERR_UNSUPPORTED, "hidden must be < 2^31");
+  if (out == nullptr || x == nullptr || weight == nullptr) {
+    return fail(KL_ERR_INVALID_ARGUMENT, "out, x and weight must be non-null");
+  }
+  if (x_row_stride < hidden && rows > 1) {
+    return fail(KL_ERR_INVALID_ARGUMENT, "x_row_stride must be >= hidden");
+  }
+  const auto s = reinterpret_cast<hipStream_t>(stream);
+  const int h = static_cast<int>(hidden);
+  switch (dtype) {
+    case KL_DTYPE_F32:
+      return launch_typed<F32>(out, x, residual, weight, rows, h, x_row_stride, eps, s);
+    case KL_DTYPE_F16:
+      return launch_typed<F16>(out, x, residual, weight, rows, h, x_row_stride, eps, s);
+    case KL_DTYPE_BF16:
+      return launch_typed<BF16>(out, x, residual, weight, rows, h, x_row_stride, eps, s);
+  }
+  return fail(KL_ERR_UNSUPPORTED, "dtype must be f32, f16 or bf16");
+}

@@ -1,0 +1,194 @@
+// PyTorch-ROCm registration of the kernel_lab operators: torch.ops.kernel_lab.*.
+//
+// Schemas are those of csrc/torch_bindings.cpp:107-113 in the reference, so
+// callers and torch.compile graphs see the same operators:
+//   rms_norm(Tensor! out, Tensor x, Tensor weight, float eps) -> ()
+//   fused_add_rms_norm(Tensor! out, Tensor x, Tensor! residual, Tensor weight, float eps) -> ()
+//   paged_decode_attention(Tensor! out, Tensor q, Tensor k_cache, Tensor v_cache,
+//                          Tensor block_table, Tensor seq_lens, float scale) -> ()
+// plus `fused_add_rmsnorm` (same schema as fused_add_rms_norm) and the overload
+// `paged_decode_attention.splits(..., int num_splits, int max_seq_len)` for
+// the split-KV controls of the reference's Triton wrapper
+// (kernel_lab/triton_kernels/paged_attention.py:176-211); 0 means "planner
+// decides" and "block-table width" respectively.
+//
+// Outputs are caller-allocated ("Tensor!" = mutated in place). The only
+// allocation here is the split-KV workspace, taken from PyTorch's caching
+// allocator on the current stream. This file is the only one that includes
+// PyTorch; it calls the kernels through the C-ABI in kernel_lab.h.
+#include <ATen/ATen.h>
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+#include <torch/library.h>
+
+#include "kernel_lab.h"
+
+namespace {
+
+kl_dtype to_kl_dtype(at::ScalarType t) {
+  switch (t) {
+    case at::kFloat:
+      return KL_DTYPE_F32;
+    case at::kHalf:
+      return KL_DTYPE_F16;
+    case at::kBFloat16:
+      return KL_DTYPE_BF16;
+    default:
+      TORCH_CHECK(false, "kernel_lab: unsupported dtype ", t);
+  }
+}
+
+void check_status(int status, const char* what) {
+  TORCH_CHECK(status == KL_OK, "kernel_lab: ", what, " failed: ", kl_status_string(status), ": ",
+              kl_last_error());
+}
+
+kl_stream_t current_stream(const at::Device& device) {
+  return reinterpret_cast<kl_stream_t>(
+      c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(device.index()).stream());
+}
+
+// Same checks as rms_norm_impl in the reference (csrc/torch_bindings.cpp:31-49).
+void rms_norm_impl(at::Tensor& out, const at::Tensor& x, at::Tensor* residual, const at::Tensor& weight,
+                   double eps) {
+  TORCH_CHECK(x.is_cuda() && weight.is_cuda() && out.is_cuda(), "tensors must be on the GPU");
+  TORCH_CHECK(x.device() == weight.device() && x.device() == out.device(), "tensors must share a device");
+  TORCH_CHECK(x.dim() >= 1 && x.stride(-1) == 1, "x must have a contiguous last dimension");
+  TORCH_CHECK(out.is_contiguous() && weight.is_contiguous(), "out and weight must be contiguous");
+  const int64_t hidden = x.size(-1);
+  TORCH_CHECK(weight.numel() == hidden, "weight size ", weight.numel(), " != hidden ", hidden);
+  TORCH_CHECK(out.sizes() == x.sizes(), "out must match x");
+  TORCH_CHECK(x.scalar_type() == weight.scalar_type() && x.scalar_type() == out.scalar_type(),
+              "x, weight and out must share a dtype");
+
+  // Rows of x may be strided (a slice); view everything as [rows, hidden].
+  const at::Tensor x2 = x.dim() == 2 ? x : x.reshape({-1, hidden});
+  TORCH_CHECK(x2.stride(-1) == 1, "x cannot be viewed as rows with a contiguous last dim");
+  void* res_ptr = nullptr;
+  if (residual != nullptr) {
+    TORCH_CHECK(residual->is_cuda() && residual->device() == x.device(), "residual must be on x's device");
+    TORCH_CHECK(residual->is_contiguous() && residual->sizes() == x.sizes() &&
+                    residual->scalar_type() == x.scalar_type(),
+                "residual must be contiguous, same shape and dtype as x");
+    res_ptr = residual->data_ptr();
+  }
+  if (x2.numel() == 0) return;
+
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+  const int64_t rows = x2.size(0);
+  const int64_t stride = rows > 1 ? x2.stride(0) : hidden;
+  check_status(kl_rms_norm(to_kl_dtype(x.scalar_type()), out.data_ptr(), x2.data_ptr(), res_ptr,
+                           weight.data_ptr(), rows, hidden, stride, static_cast<float>(eps),
+                           current_stream(x.device())),
+               "rms_norm");
+}
+
+void rms_norm(at::Tensor& out, const at::Tensor& x, const at::Tensor& weight, double eps) {
+  rms_norm_impl(out, x, nullptr, weight, eps);
+}
+
+void fused_add_rms_norm(at::Tensor& out, const at::Tensor& x, at::Tensor& residual, const at::Tensor& weight,
+                        double eps) {
+  rms_norm_impl(out, x, &residual, weight, eps);
+}
+
+// Same checks as paged_decode_attention in the reference
+// (csrc/torch_bindings.cpp:71-93), plus device agreement and max_seq_len.
+void paged_decode_impl(at::Tensor& out, const at::Tensor& q, const at::Tensor& k_cache, const at::Tensor& v_cache,
+                       const at::Tensor& block_table, const at::Tensor& seq_lens, double scale, int64_t num_splits,
+                       int64_t max_seq_len) {
+  TORCH_CHECK(q.is_cuda() && k_cache.is_cuda() && v_cache.is_cuda() && out.is_cuda() && block_table.is_cuda() &&
+                  seq_lens.is_cuda(),
+              "tensors must be on the GPU");
+  const auto dev = q.device();
+  TORCH_CHECK(k_cache.device() == dev && v_cache.device() == dev && out.device() == dev &&
+                  block_table.device() == dev && seq_lens.device() == dev,
+              "tensors must share a device");
+  TORCH_CHECK(q.dim() == 3 && k_cache.dim() == 4, "q is [batch, heads, dim]; caches are 4-D");
+  TORCH_CHECK(q.is_contiguous() && out.is_contiguous() && k_cache.is_contiguous() && v_cache.is_contiguous(),
+              "q, out and both caches must be contiguous");
+  TORCH_CHECK(k_cache.sizes() == v_cache.sizes(), "k_cache and v_cache shapes differ");
+  TORCH_CHECK(out.sizes() == q.sizes(), "out must match q");
+  TORCH_CHECK(block_table.scalar_type() == at::kInt && seq_lens.scalar_type() == at::kInt,
+              "block_table and seq_lens must be int32");
+  TORCH_CHECK(block_table.dim() == 2 && seq_lens.dim() == 1, "block_table is 2-D and seq_lens 1-D");
+  TORCH_CHECK(block_table.stride(-1) == 1 && seq_lens.is_contiguous(),
+              "block_table rows and seq_lens must be contiguous");
+  TORCH_CHECK(q.scalar_type() == k_cache.scalar_type() && q.scalar_type() == v_cache.scalar_type() &&
+                  q.scalar_type() == out.scalar_type(),
+              "q, caches and out must share a dtype");
+
+  const int batch = static_cast<int>(q.size(0));
+  const int num_q_heads = static_cast<int>(q.size(1));
+  const int head_dim = static_cast<int>(q.size(2));
+  const int page_size = static_cast<int>(k_cache.size(1));
+  const int num_kv_heads = static_cast<int>(k_cache.size(2));
+  TORCH_CHECK(k_cache.size(3) == head_dim, "cache head_dim differs from q");
+  TORCH_CHECK(num_kv_heads > 0 && num_q_heads % num_kv_heads == 0,
+              "num_q_heads must be a multiple of num_kv_heads");
+  TORCH_CHECK(block_table.size(0) == batch && seq_lens.size(0) == batch,
+              "block_table and seq_lens need one row per sequence");
+  TORCH_CHECK(num_splits >= 0 && max_seq_len >= 0, "num_splits and max_seq_len must be >= 0");
+  if (batch == 0) return;
+
+  int64_t max_pages = block_table.size(1);
+  if (max_seq_len > 0) max_pages = std::min<int64_t>(max_pages, (max_seq_len + page_size - 1) / page_size);
+  TORCH_CHECK(max_pages >= 1, "block_table needs at least one column");
+  const int64_t bt_stride = batch > 1 ? block_table.stride(0) : block_table.size(1);
+
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(dev);
+  const kl_dtype dtype = to_kl_dtype(q.scalar_type());
+  int splits = 0;
+  size_t ws_bytes = 0;
+  check_status(kl_paged_decode_plan(dtype, batch, num_q_heads, num_kv_heads, head_dim, page_size,
+                                    static_cast<int>(max_pages), static_cast<int>(num_splits), 0, &splits,
+                                    &ws_bytes),
+               "paged_decode_attention planning");
+  at::Tensor workspace;
+  if (ws_bytes > 0) {
+    workspace = at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
+  }
+  check_status(kl_paged_decode_attention(dtype, out.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                                         block_table.data_ptr<int32_t>(), seq_lens.data_ptr<int32_t>(), batch,
+                                         num_q_heads, num_kv_heads, head_dim, page_size, bt_stride,
+                                         static_cast<int>(max_pages), static_cast<float>(scale), splits,
+                                         ws_bytes > 0 ? workspace.data_ptr() : nullptr, ws_bytes,
+                                         current_stream(dev)),
+               "paged_decode_attention");
+}
+
+void paged_decode_attention(at::Tensor& out, const at::Tensor& q, const at::Tensor& k_cache,
+                            const at::Tensor& v_cache, const at::Tensor& block_table, const at::Tensor& seq_lens,
+                            double scale) {
+  paged_decode_impl(out, q, k_cache, v_cache, block_table, seq_lens, scale, 0, 0);
+}
+
+void paged_decode_attention_splits(at::Tensor& out, const at::Tensor& q, const at::Tensor& k_cache,
+                                   const at::Tensor& v_cache, const at::Tensor& block_table,
+                                   const at::Tensor& seq_lens, double scale, int64_t num_splits,
+                                   int64_t max_seq_len) {
+  paged_decode_impl(out, q, k_cache, v_cache, block_table, seq_lens, scale, num_splits, max_seq_len);
+}
+
+}  // namespace
+
+TORCH_LIBRARY(kernel_lab, m) {
+  m.def("rms_norm(Tensor! out, Tensor x, Tensor weight, float eps) -> ()");
+  m.def("fused_add_rms_norm(Tensor! out, Tensor x, Tensor! residual, Tensor weight, float eps) -> ()");
+  m.def("fused_add_rmsnorm(Tensor! out, Tensor x, Tensor! residual, Tensor weight, float eps) -> ()");
+  m.def(
+      "paged_decode_attention(Tensor! out, Tensor q, Tensor k_cache, Tensor v_cache, "
+      "Tensor block_table, Tensor seq_lens, float scale) -> ()");
+  m.def(
+      "paged_decode_attention.splits(Tensor! out, Tensor q, Tensor k_cache, Tensor v_cache, "
+      "Tensor block_table, Tensor seq_lens, float scale, int num_splits, int max_seq_len) -> ()");
+}
+
+// ROCm tensors carry PyTorch's CUDA dispatch key.
+TORCH_LIBRARY_IMPL(kernel_lab, CUDA, m) {
+  m.impl("rms_norm", &rms_norm);
+  m.impl("fused_add_rms_norm", &fused_add_rms_norm);
+  m.impl("fused_add_rmsnorm", &fused_add_rms_norm);
+  m.impl("paged_decode_attention", &paged_decode_attention);
+  m.impl("paged_decode_attention.splits", &paged_decode_attention_splits);
+}

@@ -1,0 +1,66 @@
+"""Shared test setup.
+
+* ``gpu`` marks tests that need an MI355X; everything else runs on the CPU.
+* The repository root (for ``oracle``) and ``kernel-lab_amd`` (for the
+  ``kernel_lab`` package) go on sys.path, so the tests run from a source tree
+  without installation.
+* Tolerances are the original project's table (tests/conftest.py:34-39 of
+  Markkoby3/Kernel-lab); bf16 keeps its 1.6e-2 because one bf16 ulp at |x| ~ 2
+  is already 7.8e-3.
+"""
+
+from __future__ import annotations
+
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+for p in (ROOT, ROOT / "kernel-lab_amd"):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+import torch  # noqa: E402
+
+
+def pytest_configure(config: pytest.Config) -> None:
+    config.addinivalue_line("markers", "gpu: needs an AMD Instinct GPU (MI355X) and the built HIP libraries")
+
+
+def tolerance(dtype: torch.dtype) -> dict[str, float]:
+    return {
+        torch.float32: {"atol": 1e-4, "rtol": 1e-4},
+        torch.float16: {"atol": 2e-3, "rtol": 2e-3},
+        torch.bfloat16: {"atol": 1.6e-2, "rtol": 1.6e-2},
+    }[dtype]
+
+
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+
+
+def ulp_distance(a: torch.Tensor, b: torch.Tensor) -> int:
+    """Largest distance in units in the last place between two same-dtype tensors."""
+    assert a.dtype == b.dtype and a.dtype in (torch.float16, torch.bfloat16, torch.float32)
+    itype = {torch.float16: torch.int16, torch.bfloat16: torch.int16, torch.float32: torch.int32}[a.dtype]
+    ai = a.contiguous().view(itype).to(torch.int64)
+    bi = b.contiguous().view(itype).to(torch.int64)
+    bits = 16 if itype == torch.int16 else 32
+    # Map sign-magnitude to a monotone integer line.
+    sign = 1 << (bits - 1)
+    ai = torch.where(ai < 0, -(ai + sign), ai)
+    bi = torch.where(bi < 0, -(bi + sign), bi)
+    return int((ai - bi).abs().max()) if ai.numel() else 0
+
+
+@pytest.fixture(scope="session")
+def gpu_ops():
+    """The kernel_lab ops module. Skips without a GPU; fails (never falls back)
+    when a GPU is present but the HIP libraries did not load."""
+    from kernel_lab import _native, ops
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU device")
+    if not _native.loaded():
+        pytest.fail(f"GPU present but kernel_lab native libraries missing: {_native.why_unavailable()}")
+    return ops

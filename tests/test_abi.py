@@ -1,0 +1,112 @@
+"""The C-ABI library: it loads, exports every symbol include/kernel_lab.h
+declares, and its host-only paths (status codes, argument checks, the split
+planner) behave as documented. Nothing here launches a kernel."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from kernel_lab import _native, ops
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "kernel_lab.h"
+
+pytestmark = pytest.mark.skipif(not _native.loaded(), reason=_native.why_unavailable())
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(kl_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_boundary():
+    names = declared_functions()
+    assert "kl_rms_norm" in names and "kl_paged_decode_attention" in names and "kl_paged_decode_plan" in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(_native.CORE_PATH))
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} declared in kernel_lab.h but not exported"
+
+
+def test_python_signatures_cover_the_header():
+    assert set(declared_functions()) == set(_native.SIGNATURES)
+
+
+def test_status_strings():
+    lib = _native.core()
+    assert lib.kl_status_string(0) == b"success"
+    assert b"argument" in lib.kl_status_string(1)
+    assert b"unknown" in lib.kl_status_string(99)
+    assert lib.kl_version() >= 100
+
+
+def test_rms_norm_argument_errors_need_no_gpu():
+    lib = _native.core()
+    # rows == 0 is a successful no-op, even with null pointers.
+    assert lib.kl_rms_norm(1, None, None, None, None, 0, 4096, 4096, 1e-6, None) == 0
+    assert lib.kl_rms_norm(1, None, None, None, None, 4, 4096, 4096, 1e-6, None) == 1
+    assert b"non-null" in lib.kl_last_error()
+    assert lib.kl_rms_norm(1, 16, 16, None, 16, 4, 4096, 100, 1e-6, None) == 1
+    assert b"stride" in lib.kl_last_error()
+    assert lib.kl_rms_norm(1, 16, 16, None, 16, -1, 4096, 4096, 1e-6, None) == 1
+
+
+def test_decode_argument_errors_need_no_gpu():
+    lib = _native.core()
+    # batch == 0: no-op.
+    assert lib.kl_paged_decode_attention(1, *([None] * 6), 0, 32, 8, 128, 16, 256, 256, 0.1, 0, None, 0, None) == 0
+    # Group not a divisor.
+    assert lib.kl_paged_decode_attention(1, *([None] * 6), 2, 3, 2, 32, 16, 4, 4, 0.1, 0, None, 0, None) == 1
+    assert b"multiple" in lib.kl_last_error()
+    # Unsupported head_dim.
+    assert lib.kl_paged_decode_attention(1, *([None] * 6), 2, 4, 2, 24, 16, 4, 4, 0.1, 0, None, 0, None) == 2
+
+
+@pytest.mark.parametrize(
+    ("batch", "hkv", "max_pages", "cus", "want"),
+    [
+        (64, 8, 256, 256, 1),  # 512 units already fill 256 CUs twice
+        (1, 8, 256, 256, 64),  # capped at 64 splits
+        (8, 8, 256, 256, 8),
+        (32, 8, 32, 256, 2),
+        (1, 1, 3, 256, 3),  # never more splits than pages
+        (64, 1, 512, 256, 8),
+    ],
+)
+def test_planner_fills_the_device(batch, hkv, max_pages, cus, want):
+    splits, ws = ops.plan_decode(torch.float16, batch, hkv * 4, hkv, 128, 16, max_pages, 0, cus)
+    assert splits == want
+    if splits > 1:
+        assert ws >= batch * hkv * 4 * splits * (128 + 1) * 4
+    else:
+        assert ws == 0
+
+
+@pytest.mark.parametrize(("requested", "max_pages", "want"), [(1, 5, 1), (2, 5, 2), (3, 5, 3), (5, 5, 5), (64, 5, 5), (4, 7, 4), (5, 7, 4)])
+def test_requested_splits_normalise_like_the_original(requested, max_pages, want):
+    """pages_per_split = cdiv(max_pages, S); S = cdiv(max_pages, pages_per_split)
+    (kernel_lab/triton_kernels/paged_attention.py:210-211)."""
+    splits, _ = ops.plan_decode(torch.float32, 2, 4, 2, 32, 16, max_pages, requested, 256)
+    assert splits == want
+
+
+def test_planner_rejects_bad_shapes():
+    with pytest.raises(ValueError, match="multiple"):
+        ops.plan_decode(torch.float16, 2, 3, 2, 128, 16, 4)
+    with pytest.raises(ValueError):
+        ops.plan_decode(torch.float16, 2, 4, 2, 24, 16, 4)
+
+
+def test_one_hip_runtime_in_process():
+    """The libraries bind to the HIP runtime PyTorch already loaded."""
+    maps = Path("/proc/self/maps").read_text()
+    paths = {line.split()[-1] for line in maps.splitlines() if "libamdhip64" in line}
+    assert len(paths) <= 1, paths

@@ -1,0 +1,242 @@
+"""gfx950 paged decode attention against the CPU oracle.
+
+Shapes and rules come from the original project's tests
+(tests/test_cuda_kernels.py:44-53, tests/test_paged_attention.py:12-106) and the
+measured configurations: Llama-3-8B GQA (32/8/128/16, fp16, B 1..64, ctx 512 and
+4096, split counts 1/4/16/64 and the planner), ragged-length MQA (32/1/128/16,
+bf16, B 64, L ~ U[1, 8192]) and long-context 70B-style GQA (64/8/128/16, bf16,
+B 8, ctx 32768). Spare pages hold NaN unless a test says otherwise, so a read of
+one, or masking by multiplication, shows up as NaN.
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from kernel_lab.kv_cache import build_paged_kv, device_decode_problem, random_decode_problem
+from oracle import reference as ref
+from tests.conftest import DTYPES, tolerance
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "decode_golden.npz"
+
+
+def run(ops, q, kv, **kw):
+    return ops.paged_decode_attention(q, kv.k_cache, kv.v_cache, kv.block_table, kv.seq_lens, **kw)
+
+
+def expected(q, kv, scale=None):
+    return ref.paged_decode_attention(
+        q.cpu(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table.cpu(), kv.seq_lens.cpu(), scale
+    )
+
+
+def check(got, want, dtype):
+    got = got.cpu()
+    assert torch.isfinite(got).all(), "non-finite output: a poisoned page or tail leaked in"
+    torch.testing.assert_close(got, want, **tolerance(dtype))
+
+
+# ---------------------------------------------------- original test shapes
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize(("hq", "hkv"), [(8, 8), (16, 4), (8, 1), (32, 8)])
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
+def test_native_op_shapes(gpu_ops, hq, hkv, head_dim, dtype):
+    """tests/test_cuda_kernels.py:44-53 of the original, with NaN spares."""
+    q, kv, _, _ = random_decode_problem(
+        [1, 3, 16, 17, 300, 1025], hq, hkv, head_dim, 16, dtype=dtype, device="cuda", poison=float("nan")
+    )
+    check(run(gpu_ops, q, kv), expected(q, kv), dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize(("hq", "hkv"), [(4, 4), (8, 2), (8, 1)])
+def test_split_kernel_shapes(gpu_ops, hq, hkv, dtype):
+    """tests/test_paged_attention.py:25-29: page boundaries 1, 15/16/17, 33, 70; D = 32."""
+    q, kv, _, _ = random_decode_problem([1, 15, 16, 17, 33, 70], hq, hkv, 32, 16, dtype=dtype, device="cuda")
+    check(run(gpu_ops, q, kv), expected(q, kv), dtype)
+
+
+@pytest.mark.parametrize("num_splits", [1, 2, 3, 5, 64])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_split_kv_is_exact_for_any_split_count(gpu_ops, num_splits, dtype):
+    """Splits only partition the sum; empty splits get zero weight (tests/test_paged_attention.py:32-37)."""
+    q, kv, _, _ = random_decode_problem([1, 15, 16, 17, 33, 70], 4, 2, 32, 16, dtype=dtype, device="cuda")
+    got = run(gpu_ops, q, kv, num_splits=num_splits)
+    if dtype == torch.float32:
+        torch.testing.assert_close(got.cpu(), expected(q, kv), atol=1e-5, rtol=1e-5)
+    else:
+        check(got, expected(q, kv), dtype)
+
+
+def test_agrees_with_dense_sdpa(gpu_ops):
+    q, kv, keys, values = random_decode_problem([5, 40], 8, 2, 64, 16, dtype=torch.float32, device="cuda")
+    want = ref.dense_decode_attention(q.cpu(), [k.cpu() for k in keys], [v.cpu() for v in values])
+    torch.testing.assert_close(run(gpu_ops, q, kv).cpu(), want, atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("page_size", [16, 32])
+@pytest.mark.parametrize("head_dim", [32, 64])
+def test_page_and_head_sizes(gpu_ops, page_size, head_dim, dtype):
+    q, kv, _, _ = random_decode_problem([3, 50], 4, 2, head_dim, page_size, dtype=dtype, device="cuda")
+    got = run(gpu_ops, q, kv)
+    if dtype == torch.float32:
+        torch.testing.assert_close(got.cpu(), expected(q, kv), atol=1e-5, rtol=1e-5)
+    else:
+        check(got, expected(q, kv), dtype)
+
+
+@pytest.mark.parametrize("page_size", [1, 8, 64])
+def test_other_page_sizes(gpu_ops, page_size):
+    q, kv, _, _ = random_decode_problem([3, 50, 64], 8, 2, 64, page_size, dtype=torch.float16, device="cuda")
+    check(run(gpu_ops, q, kv), expected(q, kv), torch.float16)
+
+
+@pytest.mark.parametrize("poison", [1e4, float("nan")])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_reads_only_pages_in_the_block_table(gpu_ops, poison, dtype):
+    """Spare pages poisoned (tests/test_paged_attention.py:56-62), and tails too."""
+    q, kv, _, _ = random_decode_problem(
+        [20, 9, 33], 4, 4, 32, 16, dtype=dtype, device="cuda", poison=poison, tail=poison
+    )
+    out = run(gpu_ops, q, kv)
+    assert torch.isfinite(out).all() and out.abs().max() < 10
+    check(out, expected(q, kv), dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_nan_tails_under_mfma_tiles(gpu_ops, dtype):
+    """Lengths that end mid-block at 128/16 put NaN tokens inside MFMA tiles."""
+    q, kv, _, _ = random_decode_problem(
+        [1, 5, 17, 31, 47, 100], 32, 8, 128, 16, dtype=dtype, device="cuda", poison=float("nan"), tail=float("nan")
+    )
+    check(run(gpu_ops, q, kv), expected(q, kv), dtype)
+
+
+def test_max_seq_len_bounds_work_without_changing_results(gpu_ops):
+    q, kv, _, _ = random_decode_problem([5, 20], 4, 2, 32, 16, dtype=torch.float32, device="cuda")
+    kv.block_table = torch.nn.functional.pad(kv.block_table, (0, 6))  # extra block-table columns
+    torch.testing.assert_close(run(gpu_ops, q, kv, max_seq_len=20).cpu(), expected(q, kv), atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(run(gpu_ops, q, kv).cpu(), expected(q, kv), atol=1e-5, rtol=1e-5)
+
+
+def test_strided_block_table(gpu_ops):
+    q, kv, _, _ = random_decode_problem([5, 40, 17], 8, 2, 64, 16, dtype=torch.float16, device="cuda")
+    wide = torch.zeros(3, kv.block_table.shape[1] + 5, dtype=torch.int32, device="cuda")
+    wide[:, : kv.block_table.shape[1]] = kv.block_table
+    kv.block_table = wide[:, : kv.block_table.shape[1]]  # row stride > width
+    check(run(gpu_ops, q, kv), expected(q, kv), torch.float16)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_custom_scale(gpu_ops, dtype):
+    q, kv, _, _ = random_decode_problem([12, 40], 2, 2, 32, 16, dtype=dtype, device="cuda")
+    check(run(gpu_ops, q, kv, scale=0.05), expected(q, kv, scale=0.05), dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_one_hot_attention_returns_that_value(gpu_ops, dtype):
+    """tests/test_paged_attention.py:81-91 of the original."""
+    head_dim = 32
+    keys = [torch.zeros(20, 1, head_dim)]
+    values = [torch.arange(20, dtype=torch.float32)[:, None, None].expand(20, 1, head_dim).clone()]
+    keys[0][13, 0, 0] = 100.0
+    kv = build_paged_kv([k.to("cuda", dtype) for k in keys], [v.to("cuda", dtype) for v in values], page_size=16)
+    q = torch.zeros(1, 1, head_dim, device="cuda", dtype=dtype)
+    q[0, 0, 0] = 1.0
+    out = run(gpu_ops, q, kv, scale=1.0)
+    torch.testing.assert_close(out.float(), torch.full_like(out.float(), 13.0), atol=1e-4, rtol=0)
+
+
+def test_validation(gpu_ops):
+    q, kv, _, _ = random_decode_problem([4], 3, 2, 32, 16, dtype=torch.float32, device="cuda")
+    with pytest.raises(ValueError, match="multiple"):
+        run(gpu_ops, q, kv)
+    q, kv, _, _ = random_decode_problem([4], 2, 2, 24, 16, dtype=torch.float32, device="cuda")
+    with pytest.raises(ValueError, match="power of two"):
+        run(gpu_ops, q, kv)
+    q, kv, _, _ = random_decode_problem([4], 4, 2, 32, 16, dtype=torch.float16, device="cuda")
+    with pytest.raises(RuntimeError, match="int32"):
+        torch.ops.kernel_lab.paged_decode_attention(
+            torch.empty_like(q), q, kv.k_cache, kv.v_cache, kv.block_table.long(), kv.seq_lens, 0.1
+        )
+
+
+def test_empty_sequence_gives_zeros(gpu_ops):
+    """seq_len 0 attends over nothing; the original's math (an empty weighted sum) gives 0."""
+    q, kv, _, _ = random_decode_problem([4, 9], 4, 2, 64, 16, dtype=torch.float16, device="cuda")
+    kv.seq_lens[0] = 0
+    for splits in (None, 3):
+        out = run(gpu_ops, q, kv, num_splits=splits)
+        assert torch.equal(out[0].cpu(), torch.zeros_like(out[0].cpu()))
+        want = expected(q[1:], type(kv)(kv.k_cache, kv.v_cache, kv.block_table[1:], kv.seq_lens[1:], 16))
+        check(out[1:], want, torch.float16)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_golden_vectors(gpu_ops, dtype):
+    data = np.load(GOLDEN)
+    names = sorted({k.split("/")[0] for k in data.files})
+    for name in names:
+        g = {f: data[f"{name}/{f}"] for f in ("q", "k_cache", "v_cache", "block_table", "seq_lens", "scale")}
+        q = torch.from_numpy(g["q"]).to("cuda", dtype)
+        k = torch.from_numpy(g["k_cache"]).to("cuda", dtype)
+        v = torch.from_numpy(g["v_cache"]).to("cuda", dtype)
+        bt = torch.from_numpy(g["block_table"]).cuda()
+        lens = torch.from_numpy(g["seq_lens"]).cuda()
+        out = gpu_ops.paged_decode_attention(q, k, v, bt, lens, float(g["scale"]))
+        want = torch.from_numpy(data[f"{name}/expected"]).float()
+        tol = {"atol": 1e-5, "rtol": 1e-5} if dtype == torch.float32 else tolerance(dtype)
+        torch.testing.assert_close(out.cpu().float(), want, **tol, msg=lambda m, n=name: f"{n}: {m}")
+
+
+def test_long_context(gpu_ops):
+    """tests/test_paged_attention.py:103-106: [4096, 31, 2000], 32/8/128, fp16."""
+    q, kv, _, _ = random_decode_problem([4096, 31, 2000], 32, 8, 128, 16, dtype=torch.float16, device="cuda")
+    check(run(gpu_ops, q, kv), expected(q, kv), torch.float16)
+
+
+# ------------------------------------------------ measured configurations
+
+
+@pytest.mark.parametrize("batch", [1, 8, 32, 64])
+@pytest.mark.parametrize("ctx", [512, 4096])
+def test_config2_llama3_gqa(gpu_ops, batch, ctx):
+    """32/8/128/16 fp16, NaN spares, splits {1, 4, 16, 64} and the planner."""
+    q, kv = device_decode_problem([ctx] * batch, 32, 8, 128, 16, dtype=torch.float16, seed=batch + ctx)
+    want = expected(q, kv)
+    for splits in (None, 1, 4, 16, 64):
+        check(run(gpu_ops, q, kv, num_splits=splits), want, torch.float16)
+
+
+def test_config3_ragged_mqa(gpu_ops):
+    """32/1/128/16 bf16, B 64, L ~ U[1, 8192] with page-boundary lengths, NaN spares."""
+    g = torch.Generator().manual_seed(3)
+    lens = torch.randint(1, 8193, (64,), generator=g).tolist()
+    lens[:9] = [1, 15, 16, 17, 8191, 8192, 4095, 4096, 4097]
+    q, kv = device_decode_problem(lens, 32, 1, 128, 16, dtype=torch.bfloat16, seed=3)
+    want = expected(q, kv)
+    for splits in (None, 1, 7, 64):
+        check(run(gpu_ops, q, kv, num_splits=splits), want, torch.bfloat16)
+
+
+def test_config4_long_context_gqa(gpu_ops):
+    """64/8/128/16 bf16, B 8, ctx 32768; the planner picks the splits."""
+    q, kv = device_decode_problem([32768] * 8, 64, 8, 128, 16, dtype=torch.bfloat16, seed=4)
+    got = run(gpu_ops, q, kv)
+    want = expected(q, kv)
+    check(got, want, torch.bfloat16)
+    # Against the unrounded fp32 result as well: at most one bf16 ulp-ish error.
+    want32 = ref.paged_decode_attention(
+        q.cpu().float(), kv.k_cache.cpu().float(), kv.v_cache.cpu().float(), kv.block_table.cpu(), kv.seq_lens.cpu()
+    )
+    err = (got.cpu().float() - want32).abs().max().item()
+    assert err < 1.6e-2, err

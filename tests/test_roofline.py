@@ -1,0 +1,66 @@
+"""Roofline byte/FLOP model: the original project's known answers
+(tests/test_roofline.py:9-47 of Markkoby3/Kernel-lab) plus the MI355X entry."""
+
+from __future__ import annotations
+
+import pytest
+
+from kernel_lab.bench import roofline
+
+
+def test_rms_norm_bytes_count_each_tensor_once():
+    w = roofline.rms_norm_work(rows=2, hidden=8, elem_bytes=2, fused_residual=True)
+    assert w.bytes == 2 * 8 * 2 * 4 + 8 * 2  # x, residual in; out, residual out; + weight
+    assert roofline.rms_norm_work(2, 8, 2, False).bytes == 2 * 8 * 2 * 2 + 8 * 2
+
+
+def test_decode_attention_is_memory_bound_on_every_listed_gpu():
+    work = roofline.decode_attention_work([4096] * 8, 32, 8, 128, elem_bytes=2)
+    assert 3.5 < work.intensity < 4.5  # GQA group 4: about 4 FLOPs per byte of KV
+    for gpu in roofline.GPU_PEAKS:
+        assert work.intensity < gpu.ridge_flops_per_byte
+
+
+def test_decode_kv_bytes():
+    work = roofline.decode_attention_work([10, 20], num_q_heads=4, num_kv_heads=2, head_dim=8, elem_bytes=2)
+    assert work.bytes == 2 * 30 * 2 * 8 * 2 + 2 * 2 * 4 * 8 * 2
+    assert work.flops == 4 * 30 * 4 * 8
+
+
+def test_baseline_floors():
+    """Algorithmic bytes at the headline shapes (8.0 TB/s floors in the build's targets)."""
+    rms = roofline.rms_norm_work(4096, 8192, 2, True)
+    assert rms.bytes == 268_451_840
+    dec = roofline.decode_attention_work([4096] * 64, 32, 8, 128, 2)
+    assert dec.bytes == 1_074_790_400
+    assert dec.flops == 4_294_967_296
+    assert abs(dec.bytes / (roofline.MI355X.dram_gbps * 1e9) * 1e6 - 134.35) < 0.01
+
+
+@pytest.mark.parametrize(
+    ("device", "expected"),
+    [
+        ("AMD Instinct MI355X", "MI355X"),
+        ("AMD Instinct MI300X", "MI300X"),
+        ("AMD Instinct MI300X VF", "MI300X"),
+        ("gfx950", "MI355X"),
+        ("NVIDIA H100 80GB HBM3", "H100 80GB HBM3"),
+        ("NVIDIA A100 80GB PCIe", "A100 80GB PCIe"),
+        ("NVIDIA L40", "L40"),
+        ("NVIDIA L40S", "L40S"),
+        ("Tesla T4", None),
+        ("NVIDIA H100 PCIe", "H100 PCIe"),
+        ("NVIDIA A100-SXM4-80GB", "A100-SXM4-80GB"),
+        ("NVIDIA A100-PCIE-40GB", "A100"),
+        ("NVIDIA L4", "L4"),
+        ("NVIDIA A10G", "A10G"),
+        ("NVIDIA GeForce RTX 4090", "RTX 4090"),
+    ],
+)
+def test_gpu_lookup(device, expected):
+    peak = roofline.lookup(device)
+    assert (peak.name if peak else None) == expected
+
+
+def test_mi355x_ridge():
+    assert 300 < roofline.MI355X.ridge_flops_per_byte < 330
