@@ -400,12 +400,15 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_kernel(const DecodeArgs 
 
 // ------------------------------------------------------------ VALU split path
 
-// The elements of a 16-byte slice as floats.
+// The elements of a 16-byte slice as floats. The fp32 case bit-casts the whole
+// vector: this compiler lowers __builtin_bit_cast of a single vector element
+// (`bit_cast<float>(v[i])`) to element 0 for every i.
 template <typename E>
 __device__ __forceinline__ void unpack16(u32x4 v, float (&f)[16 / E::kBytes]) {
   if constexpr (E::kBytes == 4) {
+    const f32x4 fv = __builtin_bit_cast(f32x4, v);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) f[i] = __builtin_bit_cast(float, v[i]);
+    for (int i = 0; i < 4; ++i) f[i] = fv[i];
   } else {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
