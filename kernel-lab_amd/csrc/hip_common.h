@@ -115,6 +115,66 @@ __device__ __forceinline__ float wave_sum(float v) {
   return (lane_read(v, 0) + lane_read(v, 16)) + (lane_read(v, 32) + lane_read(v, 48));
 }
 
+// Cross-row butterflies on gfx950's v_permlane{16,32}_swap. With both operands
+// equal to v, the two results hold, in some order, v of this lane and v of
+// lane ^ 16 (or lane ^ 32), so a commutative op over them is the butterfly
+// step; no LDS traffic and no lane-dependent select.
+__device__ __forceinline__ float max_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
+                                                  false, false);
+  return fmaxf(__builtin_bit_cast(float, static_cast<unsigned>(r[0])),
+               __builtin_bit_cast(float, static_cast<unsigned>(r[1])));
+}
+__device__ __forceinline__ float max_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
+                                                  false, false);
+  return fmaxf(__builtin_bit_cast(float, static_cast<unsigned>(r[0])),
+               __builtin_bit_cast(float, static_cast<unsigned>(r[1])));
+}
+__device__ __forceinline__ float sum_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
+                                                  false, false);
+  return __builtin_bit_cast(float, static_cast<unsigned>(r[0])) +
+         __builtin_bit_cast(float, static_cast<unsigned>(r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
+                                                  false, false);
+  return __builtin_bit_cast(float, static_cast<unsigned>(r[0])) +
+         __builtin_bit_cast(float, static_cast<unsigned>(r[1]));
+}
+
+// Raw buffer loads: a wave-uniform 128-bit resource (base address in SGPRs)
+// plus a 32-bit per-lane byte offset. The address never occupies VGPRs, so
+// deep software pipelines keep their loads in flight without register
+// conflicts. Dword 3 selects the 32-bit data format that untyped loads need
+// on the gfx9 family; num_records bounds the offsets to 2 GiB past the base.
+constexpr int kBufferDword3 = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), 0x7fffffff,
+                                           kBufferDword3);
+}
+
+// Cache-policy bits of the buffer instruction (gfx940+ encoding): NT marks a
+// streaming access, which measured ~13% more HBM read bandwidth than the
+// default policy for data read once.
+constexpr int kCachePolicyNT = 2;
+
+template <int POLICY = 0>
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t byte_offset) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, byte_offset, 0, POLICY));
+}
+
+// gfx950 transposing LDS read (ds_read_b64_tr_b16). Within each 16-lane row,
+// lane i receives element (i % 4) of the 8-byte chunks addressed by lanes
+// i/4, 4 + i/4, 8 + i/4 and 12 + i/4 of that row, in that order.
+__device__ __forceinline__ u32x2 lds_read_tr16(const void* p) {
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+  return __builtin_bit_cast(u32x2, v);
+}
+
 // Cross-row exchange (lane ^ 16, lane ^ 32) through the LDS crossbar.
 __device__ __forceinline__ float shfl_xor(float v, int mask) {
   const int lane = __lane_id();

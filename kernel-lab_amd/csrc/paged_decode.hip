@@ -147,13 +147,22 @@ struct Mfma<BF16> {
 // main loop, reused for the cross-wave merge afterwards.
 template <int D, int NT>
 struct MfmaLds {
-  static constexpr int kVRow = D + 4;  // elements per staged token row (pad spreads banks)
+  // Row stride of a staged token: 16 elements of pad put the 16 rows a
+  // transposing read touches on distinct 32-byte bank groups two by two.
+  static constexpr int kVRow = D + 16;
   static constexpr int kStageBytes = kWaves * kBlock * kVRow * 2;
   static constexpr int kAccBytes = (kWaves - 1) * NT * (D / 16) * 4 * 64 * 4;
   static constexpr int kMlBytes = kWaves * NT * 16 * 2 * 4;
   static constexpr int kBytes =
       kStageBytes > kAccBytes + kMlBytes ? kStageBytes : kAccBytes + kMlBytes;
 };
+
+// Register pipeline depth: blocks whose K and V are held in VGPRs at once
+// (one being processed, the rest in flight). 8 KiB per block at D = 128.
+template <int D, int NT>
+constexpr int mfma_stages() {
+  return D <= 64 ? 6 : (D <= 128 ? (NT == 1 ? 4 : 2) : 2);
+}
 
 template <typename E, int D, int NT>
 __global__ void __launch_bounds__(kThreads) decode_mfma_kernel(const DecodeArgs a) {
@@ -164,6 +173,7 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_kernel(const DecodeArgs 
   constexpr int LPT = D / 8;           // lanes per token row in the V load
   constexpr int TPL = 64 / LPT;        // tokens per V load instruction
   constexpr int VROW = MfmaLds<D, NT>::kVRow;
+  constexpr int NS = mfma_stages<D, NT>();
   __shared__ __attribute__((aligned(16))) char lds[MfmaLds<D, NT>::kBytes];
 
   const Unit u = decode_unit(a);
@@ -216,43 +226,54 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_kernel(const DecodeArgs 
   const int first = blk_begin + wave;
   const int nblk = first < blk_end ? (blk_end - first + kWaves - 1) / kWaves : 0;
 
-  // Per-lane element offsets inside a block (token row x head dims).
-  const int k_off = row * a.token_stride + 8 * grp;
+  // Per-lane byte offsets inside a block (token row x head dims), for buffer
+  // loads off a per-block wave-uniform base.
+  uint32_t k_off[KC], v_off[KC];
   const int v_tok = lane / LPT;
   const int v_dim = 8 * (lane % LPT);
-  const int v_off = v_tok * a.token_stride + v_dim;
+#pragma unroll
+  for (int c = 0; c < KC; ++c) {
+    k_off[c] = static_cast<uint32_t>((row * a.token_stride + 8 * grp + 32 * c) * static_cast<int>(sizeof(S)));
+    v_off[c] = static_cast<uint32_t>(((c * TPL + v_tok) * a.token_stride + v_dim) * static_cast<int>(sizeof(S)));
+  }
   S* stage = reinterpret_cast<S*>(lds) + wave * kBlock * VROW;
+  // Source of this lane's 8-byte chunk in the transposing V^T read: token
+  // 4grp + row/4, dims 4(row % 4) .. +3 of each 16-wide tile.
+  const S* tr_src = stage + (4 * grp + (row >> 2)) * VROW + 4 * (row & 3);
 
-  auto load_block = [&](int blk, u32x4 (&kf)[KC], u32x4 (&vf)[KC]) {
-    const int64_t page = bt[blk / bpp];
-    const int64_t base = page * a.page_stride + static_cast<int64_t>((blk % bpp) * kBlock) * a.token_stride +
-                         static_cast<int64_t>(u.kvh) * D;
-    const S* kb = kc + base;
-    const S* vb = vc + base;
-#pragma unroll
-    for (int c = 0; c < KC; ++c) kf[c] = *reinterpret_cast<const u32x4*>(kb + k_off + 32 * c);
-#pragma unroll
-    for (int c = 0; c < KC; ++c) {
-      vf[c] = *reinterpret_cast<const u32x4*>(vb + v_off + static_cast<int64_t>(c * TPL) * a.token_stride);
-    }
+  // Element offset of this wave's i-th block (wave-uniform, scalar math).
+  auto block_base = [&](int i) -> int64_t {
+    const int blk = first + kWaves * i;
+    const int pidx = blk / bpp;
+    return static_cast<int64_t>(bt[pidx]) * a.page_stride +
+           static_cast<int64_t>((blk - pidx * bpp) * kBlock) * a.token_stride + static_cast<int64_t>(u.kvh) * D;
   };
 
-  auto process_block = [&](int blk, const u32x4 (&kf)[KC], const u32x4 (&vf)[KC]) {
-    const int nvalid = u.seq_len - blk * kBlock;  // >= 1; >= 16 means all valid
+  auto load_block = [&](int64_t base, u32x4 (&kf)[KC], u32x4 (&vf)[KC]) {
+    const auto kr = make_rsrc(kc + base);
+    const auto vr = make_rsrc(vc + base);
+#pragma unroll
+    for (int c = 0; c < KC; ++c) kf[c] = buffer_load16<kCachePolicyNT>(kr, k_off[c]);
+#pragma unroll
+    for (int c = 0; c < KC; ++c) vf[c] = buffer_load16<kCachePolicyNT>(vr, v_off[c]);
+  };
+
+  auto process_block = [&](int i, const u32x4 (&kf)[KC], const u32x4 (&vf)[KC]) {
+    // Valid tokens in the block: >= 16 means all; <= 0 only for the padding
+    // slots of the last pipeline round (i >= nblk).
+    const int nvalid = i < nblk ? u.seq_len - (first + kWaves * i) * kBlock : 0;
 
     // Stage V (rows past seq_len as zeros) for the transposed reads below.
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
       const int tok = c * TPL + v_tok;
-      const u32x4 v = tok < nvalid ? vf[c] : u32x4{0, 0, 0, 0};
-      u32x2* dst = reinterpret_cast<u32x2*>(stage + tok * VROW + v_dim);
-      dst[0] = u32x2{v[0], v[1]};
-      dst[1] = u32x2{v[2], v[3]};
+      *reinterpret_cast<u32x4*>(stage + tok * VROW + v_dim) = tok < nvalid ? vf[c] : u32x4{0, 0, 0, 0};
     }
 
     // Scores: lane holds S[token 4grp + i][head row] for tile t.
     u32x2 pf[NT];
     float alpha[NT];
+    bool grew = false;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -260,68 +281,66 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_kernel(const DecodeArgs 
       for (int c = 0; c < KC; ++c) s = M::qk(kf[c], qf[t][c], s);
       float sc[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sc[i] = (4 * grp + i < nvalid) ? s[i] * a.scale_log2 : -INFINITY;
+      for (int j = 0; j < 4; ++j) sc[j] = (4 * grp + j < nvalid) ? s[j] * a.scale_log2 : -INFINITY;
       float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-      mx = fmaxf(mx, shfl_xor(mx, 16));
-      mx = fmaxf(mx, shfl_xor(mx, 32));
-      // Token 0 of every processed block is valid, so mx and m_new are finite.
+      mx = max_xor32(max_xor16(mx));
+      // A real block's token 0 is valid, so mx is finite; a padding slot has
+      // mx = -inf and comes after at least one real block, so m_new = m.
       const float m_new = fmaxf(m[t], mx);
-      alpha[t] = exp2f(m[t] - m_new);
+      grew |= m_new > m[t];
+      alpha[t] = __builtin_amdgcn_exp2f(m[t] - m_new);
       float p[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) p[i] = exp2f(sc[i] - m_new);
+      for (int j = 0; j < 4; ++j) p[j] = __builtin_amdgcn_exp2f(sc[j] - m_new);
       l[t] = l[t] * alpha[t] + ((p[0] + p[1]) + (p[2] + p[3]));
       m[t] = m_new;
       pf[t] = u32x2{pack2<E>(p[0], p[1]), pack2<E>(p[2], p[3])};
     }
-
-    // V^T as the A operand: lane holds V[token 4grp + j][dim 16dt + row].
-    const S* src = stage + (4 * grp) * VROW + row;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      const uint32_t v0 = src[0 * VROW + 16 * dt];
-      const uint32_t v1 = src[1 * VROW + 16 * dt];
-      const uint32_t v2 = src[2 * VROW + 16 * dt];
-      const uint32_t v3 = src[3 * VROW + 16 * dt];
-      const u32x2 va = {v0 | (v1 << 16), v2 | (v3 << 16)};
+    // Rescale the outputs only when some head's running max moved (alpha < 1).
+    if (__any(grew)) {
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        acc[t][dt] *= alpha[t];
-        acc[t][dt] = M::pv(va, pf[t], acc[t][dt]);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[t][dt] *= alpha[t];
       }
+    }
+
+    // V^T as the A operand: lane holds V[token 4grp + j][dim 16dt + row].
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const u32x2 va = lds_read_tr16(tr_src + 16 * dt);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) acc[t][dt] = M::pv(va, pf[t], acc[t][dt]);
     }
   };
 
   if (nblk > 0) {
-    u32x4 k0[KC], v0[KC], k1[KC], v1[KC];
-    load_block(first, k0, v0);
-    int i = 0;
-    while (true) {
-      if (i + 1 < nblk) {
-        load_block(first + (i + 1) * kWaves, k1, v1);
-        process_block(first + i * kWaves, k0, v0);
-      } else {
-        process_block(first + i * kWaves, k0, v0);
-        break;
+    // NS-stage pipeline: while block i is processed, blocks i+1 .. i+NS-1 are
+    // in flight. The loop runs a whole number of NS-block rounds with no
+    // branch inside, so the compiler's load-wait counts stay exact; slots past
+    // the last block re-read the last block (cache-resident) and process it
+    // with no valid token, which leaves the running state unchanged.
+    u32x4 kb[NS][KC], vb[NS][KC];
+    int64_t next_base = block_base(0);
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s) {
+      load_block(next_base, kb[s], vb[s]);
+      next_base = block_base(min(s + 1, nblk - 1));
+    }
+    for (int base = 0; base < nblk; base += NS) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const int i = base + s;
+        load_block(next_base, kb[(s + NS - 1) % NS], vb[(s + NS - 1) % NS]);
+        next_base = block_base(min(i + NS, nblk - 1));
+        process_block(i, kb[s], vb[s]);
       }
-      ++i;
-      if (i + 1 < nblk) {
-        load_block(first + (i + 1) * kWaves, k0, v0);
-        process_block(first + i * kWaves, k1, v1);
-      } else {
-        process_block(first + i * kWaves, k1, v1);
-        break;
-      }
-      ++i;
     }
   }
 
   // Per-wave normaliser: the four lane groups hold disjoint tokens of a head.
 #pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    l[t] += shfl_xor(l[t], 16);
-    l[t] += shfl_xor(l[t], 32);
-  }
+  for (int t = 0; t < NT; ++t) l[t] = sum_xor32(sum_xor16(l[t]));
 
   // Cross-wave merge. The LDS staging tiles are reused, so wait for every wave
   // to leave the main loop first.

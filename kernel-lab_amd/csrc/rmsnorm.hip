@@ -29,6 +29,27 @@ struct alignas(sizeof(S) * N) Pack {
   S v[N];
 };
 
+// Pack loads and stores. 16-byte packs go through non-temporal (streaming)
+// accesses: every byte is touched once, and on gfx950 the streaming policy
+// sustains markedly more HBM bandwidth than the default one.
+template <typename S, int N>
+__device__ __forceinline__ Pack<S, N> load_pack(const Pack<S, N>* p) {
+  if constexpr (sizeof(Pack<S, N>) == 16) {
+    return __builtin_bit_cast(Pack<S, N>, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p)));
+  } else {
+    return *p;
+  }
+}
+
+template <typename S, int N>
+__device__ __forceinline__ void store_pack(Pack<S, N>* p, const Pack<S, N>& v) {
+  if constexpr (sizeof(Pack<S, N>) == 16) {
+    __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v), reinterpret_cast<u32x4*>(p));
+  } else {
+    *p = v;
+  }
+}
+
 constexpr int kMaxThreads = 1024;
 
 // Workgroup-wide sum; every thread receives the same value. `scratch` holds one
@@ -75,8 +96,8 @@ __global__ void __launch_bounds__(kMaxThreads)
   for (int k = 0; k < NPACK; ++k) {
     const int p = threadIdx.x + k * nt;
     if (p < packs) {
-      a[k] = xr[p];
-      if constexpr (HAS_RES) b[k] = rr[p];
+      a[k] = load_pack(xr + p);
+      if constexpr (HAS_RES) b[k] = load_pack(rr + p);
     }
   }
 
@@ -90,7 +111,7 @@ __global__ void __launch_bounds__(kMaxThreads)
         P s;
 #pragma unroll
         for (int j = 0; j < VEC; ++j) s.v[j] = E::from_f32(E::to_f32(a[k].v[j]) + E::to_f32(b[k].v[j]));
-        rr[p] = s;
+        store_pack(rr + p, s);
 #pragma unroll
         for (int j = 0; j < VEC; ++j) f[k][j] = E::to_f32(s.v[j]);
       } else {
@@ -119,7 +140,7 @@ __global__ void __launch_bounds__(kMaxThreads)
       P o;
 #pragma unroll
       for (int j = 0; j < VEC; ++j) o.v[j] = E::from_f32((f[k][j] * rstd) * E::to_f32(w[k].v[j]));
-      orow[p] = o;
+      store_pack(orow + p, o);
     }
   }
 }
