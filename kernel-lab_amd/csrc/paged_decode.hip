@@ -143,14 +143,18 @@ struct Mfma<BF16> {
   }
 };
 
-// LDS bytes the MFMA kernel needs: the per-wave V staging tiles during the
-// main loop, reused for the cross-wave merge afterwards.
+// LDS bytes the MFMA kernel needs: the per-wave K and V staging tiles during
+// the main loop, reused for the cross-wave merge afterwards.
 template <int D, int NT>
 struct MfmaLds {
-  // Row stride of a staged token: 16 elements of pad put the 16 rows a
-  // transposing read touches on distinct 32-byte bank groups two by two.
+  // Row strides of a staged token. K: 8 elements (16 B) of pad put the 16
+  // rows one ds_read_b128 touches on distinct 16-byte bank groups. V: 16
+  // elements of pad put the 16 rows a transposing read touches on distinct
+  // 32-byte bank groups two by two.
+  static constexpr int kKRow = D + 8;
   static constexpr int kVRow = D + 16;
-  static constexpr int kStageBytes = kWaves * kBlock * kVRow * 2;
+  static constexpr int kWaveStage = kBlock * (kKRow + kVRow);  // elements per wave
+  static constexpr int kStageBytes = kWaves * kWaveStage * 2;
   static constexpr int kAccBytes = (kWaves - 1) * NT * (D / 16) * 4 * 64 * 4;
   static constexpr int kMlBytes = kWaves * NT * 16 * 2 * 4;
   static constexpr int kBytes =
@@ -172,6 +176,7 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_kernel(const DecodeArgs 
   constexpr int DT = D / 16;           // PV output tiles along head_dim
   constexpr int LPT = D / 8;           // lanes per token row in the V load
   constexpr int TPL = 64 / LPT;        // tokens per V load instruction
+  constexpr int KROW = MfmaLds<D, NT>::kKRow;
   constexpr int VROW = MfmaLds<D, NT>::kVRow;
   constexpr int NS = mfma_stages<D, NT>();
   __shared__ __attribute__((aligned(16))) char lds[MfmaLds<D, NT>::kBytes];
@@ -227,16 +232,24 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_kernel(const DecodeArgs 
   const int nblk = first < blk_end ? (blk_end - first + kWaves - 1) / kWaves : 0;
 
   // Per-lane byte offsets inside a block (token row x head dims), for buffer
-  // loads off a per-block wave-uniform base.
+  // loads off a per-block wave-uniform base. Load c covers tokens
+  // c*TPL .. c*TPL + TPL-1; lane l reads 16 bytes of token c*TPL + l/LPT.
   uint32_t k_off[KC], v_off[KC];
   const int v_tok = lane / LPT;
   const int v_dim = 8 * (lane % LPT);
 #pragma unroll
   for (int c = 0; c < KC; ++c) {
-    k_off[c] = static_cast<uint32_t>((row * a.token_stride + 8 * grp + 32 * c) * static_cast<int>(sizeof(S)));
+    k_off[c] = static_cast<uint32_t>(((c * TPL + v_tok) * a.token_stride + v_dim) * static_cast<int>(sizeof(S)));
     v_off[c] = static_cast<uint32_t>(((c * TPL + v_tok) * a.token_stride + v_dim) * static_cast<int>(sizeof(S)));
   }
-  S* stage = reinterpret_cast<S*>(lds) + wave * kBlock * VROW;
+  // K and V are both loaded row-coalesced (each 16-lane row reads 256
+  // contiguous bytes: a token's head dims), which the memory system streams
+  // markedly faster than the MFMA operand layout, and are re-laid out through
+  // this wave's LDS tiles: K rows are read back as the A operand (lane = token,
+  // 8 dims), V through the transposing read.
+  S* kstage = reinterpret_cast<S*>(lds) + wave * MfmaLds<D, NT>::kWaveStage;
+  S* stage = kstage + kBlock * KROW;
+  const S* k_src = kstage + row * KROW + 8 * grp;
   // Source of this lane's 8-byte chunk in the transposing V^T read: token
   // 4grp + row/4, dims 4(row % 4) .. +3 of each 16-wide tile.
   const S* tr_src = stage + (4 * grp + (row >> 2)) * VROW + 4 * (row & 3);
@@ -263,12 +276,18 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_kernel(const DecodeArgs 
     // slots of the last pipeline round (i >= nblk).
     const int nvalid = i < nblk ? u.seq_len - (first + kWaves * i) * kBlock : 0;
 
-    // Stage V (rows past seq_len as zeros) for the transposed reads below.
+    // Stage K and V (V rows past seq_len as zeros; K rows there only feed
+    // scores that are replaced by -inf below).
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
       const int tok = c * TPL + v_tok;
+      *reinterpret_cast<u32x4*>(kstage + tok * KROW + v_dim) = kf[c];
       *reinterpret_cast<u32x4*>(stage + tok * VROW + v_dim) = tok < nvalid ? vf[c] : u32x4{0, 0, 0, 0};
     }
+    // K as the A operand of S = K Q^T: lane holds token `row`, dims 32c + 8grp .. +7.
+    u32x4 ka[KC];
+#pragma unroll
+    for (int c = 0; c < KC; ++c) ka[c] = *reinterpret_cast<const u32x4*>(k_src + 32 * c);
 
     // Scores: lane holds S[token 4grp + i][head row] for tile t.
     u32x2 pf[NT];
@@ -278,7 +297,7 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_kernel(const DecodeArgs 
     for (int t = 0; t < NT; ++t) {
       f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int c = 0; c < KC; ++c) s = M::qk(kf[c], qf[t][c], s);
+      for (int c = 0; c < KC; ++c) s = M::qk(ka[c], qf[t][c], s);
       float sc[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) sc[j] = (4 * grp + j < nvalid) ? s[j] * a.scale_log2 : -INFINITY;
