@@ -47,7 +47,7 @@ from kernel_lab.kv_cache import device_decode_problem  # noqa: E402
 METRIC = "achieved HBM GB/s + % of peak: paged decode (B=64, ctx 4k) and add-RMSNorm"
 DECODE = {"batch": 64, "ctx": 4096, "num_q_heads": 32, "num_kv_heads": 8, "head_dim": 128, "page_size": 16}
 RMS = {"tokens": 4096, "hidden": 8192}
-TRAFFIC_FILE = ROOT / "profiles" / "traffic_decode_b64_ctx4096_fp16.txt"
+TRAFFIC_FILE = ROOT / "profiles" / "decode_b64_ctx4096_fp16.md"
 
 
 def log(msg: str) -> None:
@@ -149,8 +149,8 @@ def main(argv: list[str] | None = None) -> int:
     if args.gpus != 1 or world != 1:
         print(
             f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}): the decode and "
-            "RMSNorm kernels need no collectives, and this build runs on single-GPU boxes; see DESIGN.md for how "
-            "the path shards.",
+            "RMSNorm kernels need no collectives (decode shards by batch, KV head or page range; RMSNorm by "
+            "rows), and this build measures one GPU's share of the workload.",
             file=sys.stderr,
         )
         return 2

@@ -44,7 +44,21 @@
 namespace kl {
 namespace {
 
-constexpr int kWaves = 4;      // waves per workgroup
+// Compile-time tuning knobs (defaults are the measured best on MI355X).
+#ifndef KL_DECODE_WAVES
+#define KL_DECODE_WAVES 4
+#endif
+#ifndef KL_DECODE_STAGES
+#define KL_DECODE_STAGES 0  // register pipeline depth; 0 picks per head_dim
+#endif
+#ifndef KL_DECODE_SPLIT_ISSUE
+#define KL_DECODE_SPLIT_ISSUE 0  // issue a block's K and V loads in two bursts
+#endif
+#ifndef KL_DECODE_WAVES_PER_EU
+#define KL_DECODE_WAVES_PER_EU 1  // occupancy floor handed to the register allocator
+#endif
+
+constexpr int kWaves = KL_DECODE_WAVES;  // waves per workgroup
 constexpr int kThreads = kWaves * 64;
 constexpr int kBlock = 16;     // tokens per MFMA block
 constexpr int kMaxPlannedSplits = 64;
@@ -162,14 +176,17 @@ struct MfmaLds {
 };
 
 // Register pipeline depth: blocks whose K and V are held in VGPRs at once
-// (one being processed, the rest in flight). 8 KiB per block at D = 128.
+// (one being processed, the rest in flight); 8 KiB per block at D = 128.
+// Measured on MI355X at D = 128: 2 stages beat 3..6 (more bytes in flight
+// per wave past ~16 KiB lowers HBM throughput for this access pattern).
 template <int D, int NT>
 constexpr int mfma_stages() {
-  return D <= 64 ? 6 : (D <= 128 ? (NT == 1 ? 4 : 2) : 2);
+  if (KL_DECODE_STAGES > 0) return KL_DECODE_STAGES;
+  return D <= 64 ? 6 : 2;
 }
 
 template <typename E, int D, int NT>
-__global__ void __launch_bounds__(kThreads) decode_mfma_kernel(const DecodeArgs a) {
+__global__ void __launch_bounds__(kThreads, KL_DECODE_WAVES_PER_EU) decode_mfma_kernel(const DecodeArgs a) {
   using S = typename E::S;
   using M = Mfma<E>;
   constexpr int KC = D / 32;           // QK k-chunks; also 16-byte K and V loads per lane per block
@@ -262,27 +279,30 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_kernel(const DecodeArgs 
            static_cast<int64_t>((blk - pidx * bpp) * kBlock) * a.token_stride + static_cast<int64_t>(u.kvh) * D;
   };
 
-  auto load_block = [&](int64_t base, u32x4 (&kf)[KC], u32x4 (&vf)[KC]) {
+  auto load_k = [&](int64_t base, u32x4 (&kf)[KC]) {
     const auto kr = make_rsrc(kc + base);
-    const auto vr = make_rsrc(vc + base);
 #pragma unroll
     for (int c = 0; c < KC; ++c) kf[c] = buffer_load16<kCachePolicyNT>(kr, k_off[c]);
+  };
+  auto load_v = [&](int64_t base, u32x4 (&vf)[KC]) {
+    const auto vr = make_rsrc(vc + base);
 #pragma unroll
     for (int c = 0; c < KC; ++c) vf[c] = buffer_load16<kCachePolicyNT>(vr, v_off[c]);
   };
+  auto load_block = [&](int64_t base, u32x4 (&kf)[KC], u32x4 (&vf)[KC]) {
+    load_k(base, kf);
+    load_v(base, vf);
+  };
 
-  auto process_block = [&](int i, const u32x4 (&kf)[KC], const u32x4 (&vf)[KC]) {
+  auto process_block = [&](int i, const u32x4 (&kf)[KC], const u32x4 (&vf)[KC], auto&& mid) {
     // Valid tokens in the block: >= 16 means all; <= 0 only for the padding
     // slots of the last pipeline round (i >= nblk).
     const int nvalid = i < nblk ? u.seq_len - (first + kWaves * i) * kBlock : 0;
 
-    // Stage K and V (V rows past seq_len as zeros; K rows there only feed
-    // scores that are replaced by -inf below).
+    // Stage K (its rows past seq_len only feed scores replaced by -inf below).
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
-      const int tok = c * TPL + v_tok;
-      *reinterpret_cast<u32x4*>(kstage + tok * KROW + v_dim) = kf[c];
-      *reinterpret_cast<u32x4*>(stage + tok * VROW + v_dim) = tok < nvalid ? vf[c] : u32x4{0, 0, 0, 0};
+      *reinterpret_cast<u32x4*>(kstage + (c * TPL + v_tok) * KROW + v_dim) = kf[c];
     }
     // K as the A operand of S = K Q^T: lane holds token `row`, dims 32c + 8grp .. +7.
     u32x4 ka[KC];
@@ -324,6 +344,15 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_kernel(const DecodeArgs 
       }
     }
 
+    // Issue the next loads (the caller's hook) between the two phases, so a
+    // wave's loads go out in two smaller bursts.
+    mid();
+    // Stage V, rows past seq_len as zeros, for the transposed reads.
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+      const int tok = c * TPL + v_tok;
+      *reinterpret_cast<u32x4*>(stage + tok * VROW + v_dim) = tok < nvalid ? vf[c] : u32x4{0, 0, 0, 0};
+    }
     // V^T as the A operand: lane holds V[token 4grp + j][dim 16dt + row].
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
@@ -350,9 +379,15 @@ __global__ void __launch_bounds__(kThreads) decode_mfma_kernel(const DecodeArgs 
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
         const int i = base + s;
-        load_block(next_base, kb[(s + NS - 1) % NS], vb[(s + NS - 1) % NS]);
+        const int64_t nb = next_base;
+#if KL_DECODE_SPLIT_ISSUE
+        load_k(nb, kb[(s + NS - 1) % NS]);
+        process_block(i, kb[s], vb[s], [&] { load_v(nb, vb[(s + NS - 1) % NS]); });
+#else
+        load_block(nb, kb[(s + NS - 1) % NS], vb[(s + NS - 1) % NS]);
+        process_block(i, kb[s], vb[s], [] {});
+#endif
         next_base = block_base(min(i + NS, nblk - 1));
-        process_block(i, kb[s], vb[s]);
       }
     }
   }

