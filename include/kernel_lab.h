@@ -86,7 +86,10 @@ int kl_rms_norm(kl_dtype dtype, void* out, const void* x, void* residual, const 
  *                    (= cdiv(max_seq_len, page_size) when that is known)
  *   num_splits       requested KV splits; 0 lets the planner choose
  *   cu_count         compute units to plan for; 0 queries the current device
- *   out_num_splits   (host pointer) splits the launch will use
+ *   out_num_splits   (host pointer) uniform splits the launch will use, or 0
+ *                    when it balances pages across sequences on the device
+ *                    (chosen for fp16/bf16 when there are fewer
+ *                    (sequence, KV head) units than compute units)
  *   out_workspace    (host pointer) bytes of device workspace the launch needs
  *                    (0 when the launch needs none)
  */

@@ -184,4 +184,16 @@ __device__ __forceinline__ float shfl_xor(float v, int mask) {
 
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
+// A read-only int32 table (block tables, sequence lengths) seen through the
+// constant address space. A kernel that stores to global memory between its
+// loads otherwise loses the proof that the table is unclobbered, and the
+// compiler then fetches wave-uniform entries with vector loads whose result
+// waits (s_waitcnt vmcnt) also drain every K/V load still in flight; from the
+// constant space a uniform address becomes a scalar load. Only for memory no
+// kernel of the launch writes.
+typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
+__device__ __forceinline__ const_i32_ptr as_constant(const int32_t* p) {
+  return (const_i32_ptr)(p);
+}
+
 }  // namespace kl

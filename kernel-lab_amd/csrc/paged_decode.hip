@@ -55,13 +55,20 @@ namespace {
 #define KL_DECODE_SPLIT_ISSUE 0  // issue a block's K and V loads in two bursts
 #endif
 #ifndef KL_DECODE_WAVES_PER_EU
-#define KL_DECODE_WAVES_PER_EU 1  // occupancy floor handed to the register allocator
+#define KL_DECODE_WAVES_PER_EU 0  // occupancy floor for the register allocator; 0 picks per shape
+#endif
+#ifndef KL_DECODE_BALANCED_WG_PER_CU
+#define KL_DECODE_BALANCED_WG_PER_CU 1  // balanced-schedule workgroups per compute unit
+#endif
+#ifndef KL_DECODE_MIN_PAGES
+#define KL_DECODE_MIN_PAGES 16  // fewest pages a planned split or balanced workgroup takes
 #endif
 
 constexpr int kWaves = KL_DECODE_WAVES;  // waves per workgroup
 constexpr int kThreads = kWaves * 64;
 constexpr int kBlock = 16;     // tokens per MFMA block
 constexpr int kMaxPlannedSplits = 64;
+constexpr int kMinPagesPerSplit = KL_DECODE_MIN_PAGES;
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct DecodeArgs {
@@ -86,6 +93,7 @@ struct DecodeArgs {
   int pages_per_split;
   int head_groups;      // workgroups per (sequence, KV head, split) along the group
   int heads_per_wg;     // query heads one workgroup handles
+  int grid;             // workgroups of the balanced decode kernel (0: uniform splits)
   float scale_log2;     // scale * log2(e)
 };
 
@@ -104,7 +112,7 @@ __device__ __forceinline__ Unit decode_unit(const DecodeArgs& a) {
   idx /= a.head_groups;
   u.kvh = idx % a.num_kv_heads;
   u.b = idx / a.num_kv_heads;
-  const int raw = a.seq_lens[u.b];
+  const int raw = as_constant(a.seq_lens)[u.b];
   const int64_t cap = static_cast<int64_t>(a.max_pages) * a.page_size;
   u.seq_len = static_cast<int>(raw < cap ? raw : cap);
   const int num_pages = u.seq_len > 0 ? (u.seq_len + a.page_size - 1) / a.page_size : 0;
@@ -116,9 +124,8 @@ __device__ __forceinline__ Unit decode_unit(const DecodeArgs& a) {
 // Writes zeros for the heads of an empty sequence (seq_len <= 0). The math of
 // kernel_lab/reference.py:58-67 gives zeros there (softmax over no tokens, then
 // an empty weighted sum).
-template <typename E>
+template <typename S, typename E>
 __device__ void write_zero_heads(const DecodeArgs& a, const Unit& u, int head_dim) {
-  using S = typename E::S;
   const int h0 = u.hg * a.heads_per_wg;
   const int nh = min(a.heads_per_wg, a.group - h0);
   S* out = static_cast<S*>(a.out);
@@ -185,8 +192,35 @@ constexpr int mfma_stages() {
   return D <= 64 ? 6 : 2;
 }
 
+// Occupancy floor (waves per SIMD) handed to the register allocator. With two
+// head tiles (GQA groups of 17-32) the default allocation lands just above
+// the two-wave budget; asking for two keeps the accumulators in VGPRs, no
+// spills. Single-tile kernels run best at the allocator's own choice.
+template <int D, int NT>
+constexpr int mfma_waves_per_eu() {
+  if (KL_DECODE_WAVES_PER_EU > 0) return KL_DECODE_WAVES_PER_EU;
+  return NT == 2 ? 2 : 1;
+}
+
+// Where a segment's result goes: the normalised output (dtype) when the
+// segment covers its whole unit, else an fp32 partial and its log2-sum-exp.
+// Local head h (0 .. heads_per_wg-1) of the partial lives at o + h*o_head_stride
+// and lse + h*lse_head_stride.
+struct Dest {
+  bool final;
+  float* o;
+  float* lse;
+  int64_t o_head_stride;
+  int lse_head_stride;
+};
+
+// One unit segment on the MFMA path: pages [u.page_begin, u.page_end) of
+// KV head u.kvh, head group u.hg of sequence u.b, by all waves of the
+// workgroup. Contains two workgroup barriers, reached by every wave; on
+// return only wave 0 may still be writing the result, so a caller that runs
+// another segment must pass a barrier before touching `lds` again.
 template <typename E, int D, int NT>
-__global__ void __launch_bounds__(kThreads, KL_DECODE_WAVES_PER_EU) decode_mfma_kernel(const DecodeArgs a) {
+__device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, const Unit& u, const Dest& dst) {
   using S = typename E::S;
   using M = Mfma<E>;
   constexpr int KC = D / 32;           // QK k-chunks; also 16-byte K and V loads per lane per block
@@ -196,13 +230,6 @@ __global__ void __launch_bounds__(kThreads, KL_DECODE_WAVES_PER_EU) decode_mfma_
   constexpr int KROW = MfmaLds<D, NT>::kKRow;
   constexpr int VROW = MfmaLds<D, NT>::kVRow;
   constexpr int NS = mfma_stages<D, NT>();
-  __shared__ __attribute__((aligned(16))) char lds[MfmaLds<D, NT>::kBytes];
-
-  const Unit u = decode_unit(a);
-  if (u.page_begin >= u.page_end) {
-    if (u.split == 0 && u.seq_len <= 0 && a.num_splits == 1) write_zero_heads<E>(a, u, D);
-    return;  // a split past the end of its sequence has no work
-  }
 
   const int lane = __lane_id();
   const int wave = wave_id();
@@ -240,7 +267,7 @@ __global__ void __launch_bounds__(kThreads, KL_DECODE_WAVES_PER_EU) decode_mfma_
 
   const S* kc = static_cast<const S*>(a.k);
   const S* vc = static_cast<const S*>(a.v);
-  const int32_t* bt = a.block_table + static_cast<int64_t>(u.b) * a.bt_stride;
+  const const_i32_ptr bt = as_constant(a.block_table + static_cast<int64_t>(u.b) * a.bt_stride);
   const int bpp = a.page_size / kBlock;  // blocks per page
   const int blk_begin = u.page_begin * bpp;
   const int blk_end = min(u.page_end * bpp, (u.seq_len + kBlock - 1) / kBlock);
@@ -457,16 +484,209 @@ __global__ void __launch_bounds__(kThreads, KL_DECODE_WAVES_PER_EU) decode_mfma_
       }
       if (!valid) continue;
       const int d = 16 * dt + 4 * grp;
-      if (a.num_splits == 1) {
+      if (dst.final) {
         S* out = static_cast<S*>(a.out) + head * D + d;
         *reinterpret_cast<u32x2*>(out) = u32x2{pack2<E>(o[0], o[1]), pack2<E>(o[2], o[3])};
       } else {
-        float* op = a.o_part + (head * a.num_splits + u.split) * D + d;
+        float* op = dst.o + static_cast<int64_t>(16 * t + row) * dst.o_head_stride + d;
         *reinterpret_cast<f32x4*>(op) = f32x4{o[0], o[1], o[2], o[3]};
       }
     }
-    if (valid && a.num_splits > 1 && grp == 0) {
-      a.lse_part[head * a.num_splits + u.split] = mmax + log2f(denom);
+    if (valid && !dst.final && grp == 0) dst.lse[(16 * t + row) * dst.lse_head_stride] = mmax + log2f(denom);
+  }
+}
+
+// Uniform splits: workgroup = (sequence, KV head, head group, split), the
+// split owning pages_per_split pages (the reference's decomposition).
+template <typename E, int D, int NT>
+__global__ void __launch_bounds__(kThreads, (mfma_waves_per_eu<D, NT>())) decode_mfma_kernel(const DecodeArgs a) {
+  __shared__ __attribute__((aligned(16))) char lds[MfmaLds<D, NT>::kBytes];
+  const Unit u = decode_unit(a);
+  if (u.page_begin >= u.page_end) {
+    if (u.split == 0 && u.seq_len <= 0 && a.num_splits == 1) write_zero_heads<typename E::S, E>(a, u, D);
+    return;  // a split past the end of its sequence has no work
+  }
+  Dest dst;
+  dst.final = a.num_splits == 1;
+  const int64_t head0 = static_cast<int64_t>(u.b) * a.num_q_heads + u.kvh * a.group + u.hg * a.heads_per_wg;
+  dst.o = dst.final ? nullptr : a.o_part + (head0 * a.num_splits + u.split) * D;
+  dst.lse = dst.final ? nullptr : a.lse_part + head0 * a.num_splits + u.split;
+  dst.o_head_stride = static_cast<int64_t>(a.num_splits) * D;
+  dst.lse_head_stride = a.num_splits;
+  mfma_segment<E, D, NT>(a, lds, u, dst);
+}
+
+// ------------------------------------------------------- balanced schedule
+//
+// Work list: every (sequence b, KV head, head group) unit is cdiv(L_b, page
+// size) pages long; units are laid end to end, b-major. Workgroup w takes
+// positions [w*per, (w+1)*per) of that list, per = max(16, cdiv(total, grid)),
+// which may span the tail of one unit and the head of the next, so every
+// workgroup streams the same number of pages however uneven the lengths are.
+// Totals and prefix sums come from seq_lens on the device (no host sync).
+// A unit covered by one workgroup gets its output written directly; a unit
+// split across workgroups w0..w1 gets partials in slots w + unit (unique:
+// both ranges and units are ordered), merged by decode_merge_balanced_kernel.
+
+__device__ __forceinline__ int seq_pages(const DecodeArgs& a, int b) {
+  const int raw = a.seq_lens[b];
+  const int64_t cap = static_cast<int64_t>(a.max_pages) * a.page_size;
+  const int len = static_cast<int>(raw < cap ? raw : cap);
+  return len > 0 ? (len + a.page_size - 1) / a.page_size : 0;
+}
+
+// seq_pages for a wave-uniform b: one scalar load.
+__device__ __forceinline__ int seq_pages_uniform(const DecodeArgs& a, int b) {
+  const int raw = as_constant(a.seq_lens)[b];
+  const int64_t cap = static_cast<int64_t>(a.max_pages) * a.page_size;
+  const int len = static_cast<int>(raw < cap ? raw : cap);
+  return len > 0 ? (len + a.page_size - 1) / a.page_size : 0;
+}
+
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  const int lane = __lane_id();
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int t = __shfl_up(v, d, 64);
+    if (lane >= d) v += t;
+  }
+  return v;
+}
+
+__device__ __forceinline__ int64_t balanced_per(const DecodeArgs& a, int64_t total) {
+  return max(static_cast<int64_t>(kMinPagesPerSplit), (total + a.grid - 1) / a.grid);
+}
+
+// Pages in the whole work list. Wave-uniform; every wave computes it.
+__device__ __forceinline__ int64_t list_total(const DecodeArgs& a, int units_per_seq) {
+  const int lane = __lane_id();
+  int64_t total = 0;
+  for (int b0 = 0; b0 < a.batch; b0 += 64) {
+    const int b = b0 + lane;
+    const int pl = b < a.batch ? seq_pages(a, b) * units_per_seq : 0;
+    total += __builtin_amdgcn_readlane(wave_incl_scan(pl), 63);
+  }
+  return total;
+}
+
+// Length of the work list and the list position where sequence b's units
+// begin (b wave-uniform).
+__device__ __forceinline__ void list_prefix(const DecodeArgs& a, int units_per_seq, int b, int64_t* total,
+                                            int64_t* base) {
+  const int lane = __lane_id();
+  int64_t t = 0, pre = 0;
+  for (int b0 = 0; b0 < a.batch; b0 += 64) {
+    const int bb = b0 + lane;
+    const int pl = bb < a.batch ? seq_pages(a, bb) * units_per_seq : 0;
+    const int incl = wave_incl_scan(pl);
+    if (b >= b0 && b < b0 + 64) pre = t + __builtin_amdgcn_readlane(incl - pl, b - b0);
+    t += __builtin_amdgcn_readlane(incl, 63);
+  }
+  *total = t;
+  *base = pre;
+}
+
+// Where workgroup `wg` starts: its first list position `pos` (wg * per), the
+// first pages-bearing sequence whose units hold it (batch when pos is past the
+// end) and the list position where that sequence's units begin. One pass over
+// seq_lens when the batch fits a wave, two otherwise. All results uniform.
+struct Start {
+  int64_t total, per, pos, base;
+  int b;
+};
+
+__device__ __forceinline__ Start schedule_start(const DecodeArgs& a, int units_per_seq, int wg) {
+  const int lane = __lane_id();
+  Start s;
+  if (a.batch <= 64) {
+    const int pl = lane < a.batch ? seq_pages(a, lane) * units_per_seq : 0;
+    const int incl = wave_incl_scan(pl);
+    s.total = __builtin_amdgcn_readlane(incl, 63);
+    s.per = balanced_per(a, s.total);
+    s.pos = static_cast<int64_t>(wg) * s.per;
+    const uint64_t hit = __ballot(incl > s.pos);
+    if (hit == 0) {
+      s.b = a.batch;
+      s.base = s.total;
+    } else {
+      const int j = __builtin_ctzll(hit);
+      s.b = j;
+      s.base = __builtin_amdgcn_readlane(incl - pl, j);
+    }
+  } else {
+    s.total = list_total(a, units_per_seq);
+    s.per = balanced_per(a, s.total);
+    s.pos = static_cast<int64_t>(wg) * s.per;
+    s.b = a.batch;
+    s.base = 0;
+    for (int b0 = 0; b0 < a.batch; b0 += 64) {
+      const int b = b0 + lane;
+      const int pl = b < a.batch ? seq_pages(a, b) * units_per_seq : 0;
+      const int incl = wave_incl_scan(pl);
+      const int chunk = __builtin_amdgcn_readlane(incl, 63);
+      if (s.base + chunk > s.pos) {
+        const int j = __builtin_ctzll(__ballot(s.base + incl > s.pos));
+        s.b = b0 + j;
+        s.base += __builtin_amdgcn_readlane(incl - pl, j);
+        break;
+      }
+      s.base += chunk;
+    }
+  }
+  s.b = __builtin_amdgcn_readfirstlane(s.b);
+  return s;
+}
+
+template <typename E, int D, int NT>
+__global__ void __launch_bounds__(kThreads, (mfma_waves_per_eu<D, NT>()))
+    decode_mfma_balanced_kernel(const DecodeArgs a) {
+  __shared__ __attribute__((aligned(16))) char lds[MfmaLds<D, NT>::kBytes];
+  const int hp = a.num_kv_heads * a.head_groups;  // units per sequence
+  const Start st = schedule_start(a, hp, blockIdx.x);
+  int64_t pos = st.pos;
+  const int64_t end = min(pos + st.per, st.total);
+  int b = st.b;
+  int64_t base = st.base;
+
+  while (pos < end && b < a.batch) {
+    // b is pages-bearing: the start and the advance below skip empty sequences.
+    const int n = seq_pages_uniform(a, b);
+    const int r = static_cast<int>((pos - base) / n);
+    const int page0 = static_cast<int>(pos - base - static_cast<int64_t>(r) * n);
+    const int64_t unit_base = base + static_cast<int64_t>(r) * n;
+    const int page1 = static_cast<int>(min(static_cast<int64_t>(n), end - unit_base));
+
+    // The unit is wave-uniform, but the compiler cannot prove it through the
+    // scan above; without readfirstlane the buffer descriptors built from it
+    // land in VGPRs and every K/V load becomes a per-lane waterfall loop.
+    Unit u;
+    u.b = __builtin_amdgcn_readfirstlane(b);
+    u.kvh = __builtin_amdgcn_readfirstlane(r / a.head_groups);
+    u.hg = __builtin_amdgcn_readfirstlane(r % a.head_groups);
+    u.split = 0;
+    const int raw = as_constant(a.seq_lens)[u.b];
+    const int64_t cap = static_cast<int64_t>(a.max_pages) * a.page_size;
+    u.seq_len = __builtin_amdgcn_readfirstlane(static_cast<int>(raw < cap ? raw : cap));
+    u.page_begin = __builtin_amdgcn_readfirstlane(page0);
+    u.page_end = __builtin_amdgcn_readfirstlane(page1);
+
+    const int64_t slot = static_cast<int64_t>(blockIdx.x) + static_cast<int64_t>(b) * hp + r;
+    Dest dst;
+    dst.final = page0 == 0 && page1 == n;
+    dst.o = a.o_part + slot * a.heads_per_wg * D;
+    dst.lse = a.lse_part + slot * a.heads_per_wg;
+    dst.o_head_stride = D;
+    dst.lse_head_stride = 1;
+
+    __syncthreads();  // the previous segment's wave 0 may still read LDS
+    mfma_segment<E, D, NT>(a, lds, u, dst);
+
+    pos = unit_base + page1;
+    if (r == hp - 1 && page1 == n) {  // this sequence's units are done: next non-empty one
+      base += static_cast<int64_t>(n) * hp;
+      do {
+        b = __builtin_amdgcn_readfirstlane(b + 1);
+      } while (b < a.batch && seq_pages_uniform(a, b) == 0);
     }
   }
 }
@@ -518,7 +738,7 @@ __global__ void __launch_bounds__(kThreads) decode_valu_kernel(const DecodeArgs 
 
   const Unit u = decode_unit(a);
   if (u.page_begin >= u.page_end) {
-    if (u.split == 0 && u.seq_len <= 0 && a.num_splits == 1) write_zero_heads<E>(a, u, D);
+    if (u.split == 0 && u.seq_len <= 0 && a.num_splits == 1) write_zero_heads<typename E::S, E>(a, u, D);
     return;
   }
   const int lane = __lane_id();
@@ -699,6 +919,58 @@ __global__ void __launch_bounds__(64) decode_merge_kernel(const DecodeArgs a, in
   }
 }
 
+// Merge for the balanced schedule: one wave per (sequence, query head). Units
+// that one workgroup covered were written by the decode kernel; a unit spread
+// over workgroups w0..w1 is combined from slots w + unit by the LSE rule; an
+// empty sequence (no units) gets zeros here.
+template <typename E>
+__global__ void __launch_bounds__(64) decode_merge_balanced_kernel(const DecodeArgs a, int head_dim) {
+  using S = typename E::S;
+  const int lane = __lane_id();
+  const int b = blockIdx.x / a.num_q_heads;
+  const int head = blockIdx.x % a.num_q_heads;
+  const int kvh = head / a.group;
+  const int hl = head % a.group;
+  const int hg = hl / a.heads_per_wg;
+  const int hloc = hl % a.heads_per_wg;
+  const int hp = a.num_kv_heads * a.head_groups;
+  const int n = seq_pages_uniform(a, b);
+  S* out = static_cast<S*>(a.out) + (static_cast<int64_t>(b) * a.num_q_heads + head) * head_dim;
+  if (n == 0) {
+    // No cached token: the softmax-weighted sum over no values is zero.
+    for (int d = lane; d < head_dim; d += 64) out[d] = E::from_f32(0.0f);
+    return;
+  }
+  int64_t total, base;  // list length; list position of sequence b's first unit
+  list_prefix(a, hp, b, &total, &base);
+  const int64_t per = balanced_per(a, total);
+  const int r = kvh * a.head_groups + hg;
+  const int64_t unit_base = base + static_cast<int64_t>(r) * n;
+  const int64_t w0 = unit_base / per;
+  const int64_t w1 = (unit_base + n - 1) / per;
+  if (w0 == w1) return;
+  const int64_t uidx = static_cast<int64_t>(b) * hp + r;
+  const float* lse = a.lse_part + hloc;
+  const float* op = a.o_part + static_cast<int64_t>(hloc) * head_dim;
+  const int64_t stride_l = a.heads_per_wg;
+  const int64_t stride_o = static_cast<int64_t>(a.heads_per_wg) * head_dim;
+
+  const int nw = static_cast<int>(w1 - w0) + 1;
+  lse += (w0 + uidx) * stride_l;
+  op += (w0 + uidx) * stride_o;
+  float mx = -INFINITY;
+  for (int w = lane; w < nw; w += 64) mx = fmaxf(mx, lse[w * stride_l]);
+  mx = wave_max(mx);
+  float den = 0.0f;
+  for (int w = lane; w < nw; w += 64) den += exp2f(lse[w * stride_l] - mx);
+  den = wave_sum(den);
+  for (int d = lane; d < head_dim; d += 64) {
+    float num = 0.0f;
+    for (int w = 0; w < nw; ++w) num += exp2f(lse[w * stride_l] - mx) * op[w * stride_o + d];
+    out[d] = E::from_f32(num / den);
+  }
+}
+
 // -------------------------------------------------------------- host side
 
 bool mfma_path(kl_dtype dtype, int head_dim, int page_size) {
@@ -738,13 +1010,16 @@ void head_tiling(kl_dtype dtype, int head_dim, int page_size, int group, int* pe
 }
 
 struct Plan {
-  int num_splits;
+  int num_splits;       // uniform splits; 0 with the balanced schedule
   int pages_per_split;
   int heads_per_wg;
   int head_groups;
+  int grid;             // balanced-schedule workgroups; 0 for uniform splits
   size_t o_bytes;
   size_t ws_bytes;
 };
+
+constexpr int kBalancedWgPerCu = KL_DECODE_BALANCED_WG_PER_CU;
 
 constexpr size_t kAlign = 256;
 size_t align_up(size_t n) { return (n + kAlign - 1) / kAlign * kAlign; }
@@ -767,14 +1042,33 @@ int make_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads, int 
   const int group = num_q_heads / num_kv_heads;
   head_tiling(dtype, head_dim, page_size, group, &p->heads_per_wg, &p->head_groups);
   const int pages = std::max(max_pages, 1);
+  p->grid = 0;
+  const int cus = cu_count > 0 ? cu_count : 256;
+  const int64_t units = std::max<int64_t>(1, static_cast<int64_t>(batch) * num_kv_heads * p->head_groups);
+  if (num_splits == 0 && mfma_path(dtype, head_dim, page_size) && units < cus) {
+    // Fewer units than CUs: split them, balanced across sequences on the device.
+    const int64_t upper = units * pages;  // list length if every sequence were full
+    const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(cdiv(upper, kMinPagesPerSplit),
+                                                                static_cast<int64_t>(cus) * kBalancedWgPerCu));
+    p->grid = static_cast<int>(grid);
+    p->num_splits = 0;
+    p->pages_per_split = 0;
+    const size_t slots = static_cast<size_t>(grid) + static_cast<size_t>(units);
+    p->o_bytes = align_up(slots * p->heads_per_wg * head_dim * sizeof(float));
+    p->ws_bytes = p->o_bytes + align_up(slots * p->heads_per_wg * sizeof(float));
+    return ok();
+  }
   int s = num_splits;
   if (s == 0) {
-    // About two workgroups per compute unit, never more splits than pages
-    // (choose_num_splits, kernel_lab/triton_kernels/paged_attention.py:169-173).
-    const int cus = cu_count > 0 ? cu_count : 256;
-    const int64_t units = std::max<int64_t>(1, static_cast<int64_t>(batch) * num_kv_heads * p->head_groups);
-    const int64_t wanted = cdiv(2LL * cus, units);
-    s = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>({wanted, pages, kMaxPlannedSplits})));
+    // Enough splits for about one workgroup per compute unit, each split at
+    // least kMinPagesPerSplit pages, never more than 64 (the rule of
+    // choose_num_splits, kernel_lab/triton_kernels/paged_attention.py:169-173,
+    // retuned on MI355X: one 4-wave workgroup per CU beat two for every split
+    // count measured, and splits under 16 pages lose more to the merge than
+    // they gain in parallelism).
+    const int64_t wanted = cdiv(cus, units);
+    const int64_t cap = std::max<int64_t>(1, std::min<int64_t>(cdiv(pages, kMinPagesPerSplit), kMaxPlannedSplits));
+    s = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(wanted, cap)));
   }
   // Normalise: drop splits no sequence can reach (paged_attention.py:210-211).
   const int pps = static_cast<int>(cdiv(pages, s));
@@ -848,7 +1142,41 @@ int launch_split(const DecodeArgs& a, int head_dim, bool mfma, unsigned grid, hi
 }
 
 template <typename E>
+int launch_balanced(const DecodeArgs& a, int head_dim, hipStream_t stream) {
+  if constexpr (!std::is_same_v<E, F32>) {
+    const unsigned grid = static_cast<unsigned>(a.grid);
+    const bool two = a.heads_per_wg > 16;
+    switch (head_dim) {
+      case 32:
+        two ? decode_mfma_balanced_kernel<E, 32, 2><<<grid, kThreads, 0, stream>>>(a)
+            : decode_mfma_balanced_kernel<E, 32, 1><<<grid, kThreads, 0, stream>>>(a);
+        break;
+      case 64:
+        two ? decode_mfma_balanced_kernel<E, 64, 2><<<grid, kThreads, 0, stream>>>(a)
+            : decode_mfma_balanced_kernel<E, 64, 1><<<grid, kThreads, 0, stream>>>(a);
+        break;
+      case 128:
+        two ? decode_mfma_balanced_kernel<E, 128, 2><<<grid, kThreads, 0, stream>>>(a)
+            : decode_mfma_balanced_kernel<E, 128, 1><<<grid, kThreads, 0, stream>>>(a);
+        break;
+      case 256:
+        decode_mfma_balanced_kernel<E, 256, 1><<<grid, kThreads, 0, stream>>>(a);
+        break;
+      default:
+        return fail(KL_ERR_UNSUPPORTED, "no MFMA kernel for this head_dim");
+    }
+    int st = check_launch("paged decode balanced kernel launch");
+    if (st != KL_OK) return st;
+    decode_merge_balanced_kernel<E>
+        <<<static_cast<unsigned>(static_cast<int64_t>(a.batch) * a.num_q_heads), 64, 0, stream>>>(a, head_dim);
+    return check_launch("paged decode balanced merge kernel launch");
+  }
+  return fail(KL_ERR_UNSUPPORTED, "the balanced schedule needs fp16 or bf16");
+}
+
+template <typename E>
 int launch_typed(DecodeArgs& a, int head_dim, bool mfma, hipStream_t stream) {
+  if (a.grid > 0) return launch_balanced<E>(a, head_dim, stream);
   const int64_t wgs = static_cast<int64_t>(a.batch) * a.num_kv_heads * a.head_groups * a.num_splits;
   if (wgs > 0x7fffffffLL) return fail(KL_ERR_UNSUPPORTED, "too many workgroups");
   int st = launch_split<E>(a, head_dim, mfma, static_cast<unsigned>(wgs), stream);
@@ -933,6 +1261,7 @@ extern "C" int kl_paged_decode_attention(kl_dtype dtype, void* out, const void* 
   a.num_splits = p.num_splits;
   a.pages_per_split = p.pages_per_split;
   a.head_groups = p.head_groups;
+  a.grid = p.grid;
   a.heads_per_wg = p.heads_per_wg;
   a.scale_log2 = scale * kLog2e;
 

@@ -73,21 +73,41 @@ def test_decode_argument_errors_need_no_gpu():
 @pytest.mark.parametrize(
     ("batch", "hkv", "max_pages", "cus", "want"),
     [
-        (64, 8, 256, 256, 1),  # 512 units already fill 256 CUs twice
-        (1, 8, 256, 256, 64),  # capped at 64 splits
-        (8, 8, 256, 256, 8),
-        (32, 8, 32, 256, 2),
-        (1, 1, 3, 256, 3),  # never more splits than pages
-        (64, 1, 512, 256, 8),
+        (64, 8, 256, 256, 1),  # 512 units already fill 256 CUs
+        (32, 8, 256, 256, 1),  # 256 units: one per CU
+        (1, 8, 256, 256, 16),  # 32 would be wanted; splits keep >= 16 pages
+        (8, 8, 256, 256, 4),
+        (8, 8, 2048, 256, 4),
+        (1, 1, 3, 256, 1),  # a 3-page table is one split
+        (1, 1, 8192, 256, 64),  # capped at 64 splits
+        (64, 1, 512, 256, 4),
     ],
 )
 def test_planner_fills_the_device(batch, hkv, max_pages, cus, want):
-    splits, ws = ops.plan_decode(torch.float16, batch, hkv * 4, hkv, 128, 16, max_pages, 0, cus)
+    """Uniform-split rule (fp32 takes it at every size)."""
+    splits, ws = ops.plan_decode(torch.float32, batch, hkv * 4, hkv, 128, 16, max_pages, 0, cus)
     assert splits == want
     if splits > 1:
         assert ws >= batch * hkv * 4 * splits * (128 + 1) * 4
     else:
         assert ws == 0
+
+
+@pytest.mark.parametrize(
+    ("batch", "hkv", "max_pages", "balanced"),
+    [(64, 8, 256, False), (32, 8, 256, False), (8, 8, 256, True), (1, 8, 32, True), (64, 1, 512, True)],
+)
+def test_planner_balances_when_units_do_not_fill_the_device(batch, hkv, max_pages, balanced):
+    """fp16/bf16 with fewer (sequence, KV head) units than CUs: pages are balanced
+    across sequences on the device (reported as 0 splits) with a workspace for
+    one partial per workgroup and unit."""
+    splits, ws = ops.plan_decode(torch.float16, batch, hkv * 4, hkv, 128, 16, max_pages, 0, 256)
+    if balanced:
+        units = batch * hkv
+        grid = min(256, -(-units * max_pages // 16))
+        assert splits == 0 and ws >= (grid + units) * 4 * (128 + 1) * 4
+    else:
+        assert splits == 1 and ws == 0
 
 
 @pytest.mark.parametrize(("requested", "max_pages", "want"), [(1, 5, 1), (2, 5, 2), (3, 5, 3), (5, 5, 5), (64, 5, 5), (4, 7, 4), (5, 7, 4)])

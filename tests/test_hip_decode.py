@@ -240,3 +240,45 @@ def test_config4_long_context_gqa(gpu_ops):
     )
     err = (got.cpu().float() - want32).abs().max().item()
     assert err < 1.6e-2, err
+
+
+# ------------------------------------------- balanced schedule (planner path)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_balanced_schedule_many_short_sequences(gpu_ops, dtype):
+    """240 one-page units: each workgroup's range spans many whole units."""
+    g = torch.Generator().manual_seed(11)
+    lens = torch.randint(1, 17, (30,), generator=g).tolist()
+    q, kv, _, _ = random_decode_problem(lens, 32, 8, 128, 16, dtype=dtype, device="cuda", poison=float("nan"))
+    check(run(gpu_ops, q, kv), expected(q, kv), dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize(("hq", "hkv"), [(32, 1), (8, 2), (64, 8)])
+def test_balanced_schedule_ragged_lengths(gpu_ops, dtype, hq, hkv):
+    """One long sequence among short and empty-page-boundary ones: units split
+    across workgroups, ranges spanning unit and sequence boundaries."""
+    lens = [6000, 1, 5, 300, 17, 16, 33, 2048, 15, 1]
+    q, kv, _, _ = random_decode_problem(lens, hq, hkv, 128, 16, dtype=dtype, device="cuda", poison=float("nan"))
+    check(run(gpu_ops, q, kv), expected(q, kv), dtype)
+
+
+def test_balanced_schedule_with_empty_sequences(gpu_ops):
+    q, kv, _, _ = random_decode_problem([300, 7, 1000, 9], 16, 4, 64, 16, dtype=torch.float16, device="cuda")
+    kv.seq_lens[1] = 0
+    kv.seq_lens[3] = 0
+    out = run(gpu_ops, q, kv)
+    assert torch.equal(out[1].cpu(), torch.zeros_like(out[1].cpu()))
+    assert torch.equal(out[3].cpu(), torch.zeros_like(out[3].cpu()))
+    keep = [0, 2]
+    sub = type(kv)(kv.k_cache, kv.v_cache, kv.block_table[keep], kv.seq_lens[keep], 16)
+    check(out[keep], expected(q[keep], sub), torch.float16)
+
+
+def test_planner_and_uniform_splits_agree(gpu_ops):
+    """The balanced schedule and uniform splits partition the same sum."""
+    q, kv, _, _ = random_decode_problem([5000, 3, 700], 32, 8, 128, 16, dtype=torch.float32, device="cuda")
+    a = run(gpu_ops, q.half(), type(kv)(kv.k_cache.half(), kv.v_cache.half(), kv.block_table, kv.seq_lens, 16))
+    b = run(gpu_ops, q.half(), type(kv)(kv.k_cache.half(), kv.v_cache.half(), kv.block_table, kv.seq_lens, 16), num_splits=7)
+    torch.testing.assert_close(a.float().cpu(), b.float().cpu(), atol=2e-3, rtol=2e-3)

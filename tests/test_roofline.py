@@ -64,3 +64,39 @@ def test_gpu_lookup(device, expected):
 
 def test_mi355x_ridge():
     assert 300 < roofline.MI355X.ridge_flops_per_byte < 330
+
+
+def test_markdown_marks_skips_and_wrong_results():
+    from kernel_lab.bench.__main__ import Row, to_markdown
+
+    rows = [
+        Row("k", "s", "torch", 10.0, 100.0, 50.0, 1.0, 0.0),
+        Row("k", "s", "bad", None, None, None, None, 0.5, "WRONG RESULT, not timed"),
+    ]
+    text = to_markdown(rows, "### test")
+    assert "| k | s | torch | 10.0 | 100.0 | 50.0% | 1.0x | 0.0e+00 |" in text
+    assert "bad (WRONG RESULT, not timed)" in text
+
+
+def test_cli_without_gpu_exits_cleanly(capsys):
+    import torch
+
+    from kernel_lab.bench.__main__ import main
+
+    if torch.cuda.is_available():
+        pytest.skip("GPU present")
+    assert main(["rmsnorm"]) == 2
+    assert "No GPU device" in capsys.readouterr().err
+
+
+def test_decode_cases_cover_the_measured_configs():
+    import torch
+
+    from kernel_lab.bench.__main__ import decode_cases
+
+    labels = [c[0] for c in decode_cases(torch.float16)]
+    assert "32/8/128 b64 ctx4096" in labels and "32/8/128 b1 ctx512" in labels
+    assert any("ragged" in s for s in labels) and "64/8/128 b8 ctx131072" in labels
+    ragged = next(c for c in decode_cases(torch.float16) if "ragged" in c[0])
+    assert ragged[2:] == (32, 1, torch.bfloat16) and len(ragged[1]) == 64
+    assert 1 <= min(ragged[1]) and max(ragged[1]) <= 8192
