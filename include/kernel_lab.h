@@ -33,6 +33,9 @@ typedef enum kl_dtype {
   KL_DTYPE_BF16 = 2
 } kl_dtype;
 
+/* num_splits value asking paged decode for the device-balanced schedule. */
+#define KL_SPLITS_BALANCED (-1)
+
 /*
  * Status codes. The reference launchers return cudaError_t and signal
  * unsupported shapes with cudaErrorInvalidValue (csrc/paged_attention.cu:157,
@@ -84,7 +87,9 @@ int kl_rms_norm(kl_dtype dtype, void* out, const void* x, void* residual, const 
  *
  *   max_pages        block-table columns any sequence may use
  *                    (= cdiv(max_seq_len, page_size) when that is known)
- *   num_splits       requested KV splits; 0 lets the planner choose
+ *   num_splits       requested KV splits; 0 lets the planner choose;
+ *                    KL_SPLITS_BALANCED asks for the balanced schedule at any
+ *                    batch size (fp16/bf16 MFMA shapes; elsewhere it acts as 0)
  *   cu_count         compute units to plan for; 0 queries the current device
  *   out_num_splits   (host pointer) uniform splits the launch will use, or 0
  *                    when it balances pages across sequences on the device
@@ -111,7 +116,9 @@ int kl_paged_decode_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_
  * block_table[b, 0 .. cdiv(seq_lens[b], page_size)). Entries past that and
  * pages not named there are never read. num_q_heads must be a multiple of
  * num_kv_heads (grouped-query attention). `scale` multiplies q.k.
- * num_splits == 0 lets the planner choose. The workspace must hold at least
+ * num_splits == 0 lets the planner choose; KL_SPLITS_BALANCED (-1) cuts the
+ * pages of all sequences into equal per-workgroup ranges on the device, which
+ * suits batches of very uneven lengths. The workspace must hold at least
  * the bytes kl_paged_decode_plan reports for the same arguments; it may be
  * NULL when that is 0. batch == 0 is a successful no-op.
  */

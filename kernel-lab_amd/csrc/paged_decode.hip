@@ -60,6 +60,9 @@ namespace {
 #ifndef KL_DECODE_BALANCED_WG_PER_CU
 #define KL_DECODE_BALANCED_WG_PER_CU 1  // balanced-schedule workgroups per compute unit
 #endif
+#ifndef KL_DECODE_BALANCE_ALWAYS
+#define KL_DECODE_BALANCE_ALWAYS 0  // balanced schedule also when units fill the device
+#endif
 #ifndef KL_DECODE_MIN_PAGES
 #define KL_DECODE_MIN_PAGES 16  // fewest pages a planned split or balanced workgroup takes
 #endif
@@ -1032,7 +1035,9 @@ int make_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads, int 
   if (num_q_heads % num_kv_heads != 0) {
     return fail(KL_ERR_INVALID_ARGUMENT, "num_q_heads must be a multiple of num_kv_heads");
   }
-  if (num_splits < 0) return fail(KL_ERR_INVALID_ARGUMENT, "num_splits must be >= 0");
+  if (num_splits < KL_SPLITS_BALANCED) {
+    return fail(KL_ERR_INVALID_ARGUMENT, "num_splits must be >= 0, or KL_SPLITS_BALANCED (-1)");
+  }
   if (dtype != KL_DTYPE_F32 && dtype != KL_DTYPE_F16 && dtype != KL_DTYPE_BF16) {
     return fail(KL_ERR_UNSUPPORTED, "dtype must be f32, f16 or bf16");
   }
@@ -1045,11 +1050,14 @@ int make_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads, int 
   p->grid = 0;
   const int cus = cu_count > 0 ? cu_count : 256;
   const int64_t units = std::max<int64_t>(1, static_cast<int64_t>(batch) * num_kv_heads * p->head_groups);
-  if (num_splits == 0 && mfma_path(dtype, head_dim, page_size) && units < cus) {
-    // Fewer units than CUs: split them, balanced across sequences on the device.
+  const bool mfma = mfma_path(dtype, head_dim, page_size);
+  if (num_splits == KL_SPLITS_BALANCED && !mfma) num_splits = 0;  // the VALU path has uniform splits only
+  if (mfma && (num_splits == KL_SPLITS_BALANCED || (num_splits == 0 && (units < cus || KL_DECODE_BALANCE_ALWAYS)))) {
+    // Requested, or fewer units than CUs: pages balanced across sequences on the device.
     const int64_t upper = units * pages;  // list length if every sequence were full
-    const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(cdiv(upper, kMinPagesPerSplit),
-                                                                static_cast<int64_t>(cus) * kBalancedWgPerCu));
+    const int64_t grid = std::max<int64_t>(
+        1, std::min<int64_t>({cdiv(upper, kMinPagesPerSplit),
+                              std::max<int64_t>(static_cast<int64_t>(cus) * kBalancedWgPerCu, units), 0x7fffffffLL}));
     p->grid = static_cast<int>(grid);
     p->num_splits = 0;
     p->pages_per_split = 0;

@@ -128,7 +128,8 @@ void paged_decode_impl(at::Tensor& out, const at::Tensor& q, const at::Tensor& k
               "num_q_heads must be a multiple of num_kv_heads");
   TORCH_CHECK(block_table.size(0) == batch && seq_lens.size(0) == batch,
               "block_table and seq_lens need one row per sequence");
-  TORCH_CHECK(num_splits >= 0 && max_seq_len >= 0, "num_splits and max_seq_len must be >= 0");
+  TORCH_CHECK(num_splits >= KL_SPLITS_BALANCED && max_seq_len >= 0,
+              "num_splits must be >= 0 or -1 (balanced), max_seq_len >= 0");
   if (batch == 0) return;
 
   int64_t max_pages = block_table.size(1);
@@ -151,8 +152,9 @@ void paged_decode_impl(at::Tensor& out, const at::Tensor& q, const at::Tensor& k
   check_status(kl_paged_decode_attention(dtype, out.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
                                          block_table.data_ptr<int32_t>(), seq_lens.data_ptr<int32_t>(), batch,
                                          num_q_heads, num_kv_heads, head_dim, page_size, bt_stride,
-                                         static_cast<int>(max_pages), static_cast<float>(scale), splits,
-                                         ws_bytes > 0 ? workspace.data_ptr() : nullptr, ws_bytes,
+                                         static_cast<int>(max_pages), static_cast<float>(scale),
+                                         static_cast<int>(num_splits), ws_bytes > 0 ? workspace.data_ptr() : nullptr,
+                                         ws_bytes,
                                          current_stream(dev)),
                "paged_decode_attention");
 }

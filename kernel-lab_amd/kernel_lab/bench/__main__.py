@@ -204,6 +204,7 @@ def decode_cases(dtype: torch.dtype) -> list[tuple[str, list[int], int, int, tor
     # One long sequence among short ones: splits sized from the block table's
     # width leave most of the work to the long sequence's few workgroups.
     cases.append(("32/8/128 b16 skewed 1x65536+15x1024", [65536] + [1024] * 15, 32, 8, dtype))
+    cases.append(("32/8/128 b64 skewed 1x65536+63x2048", [65536] + [2048] * 63, 32, 8, dtype))
     for ctx in (32768, 131072):
         cases.append((f"64/8/128 b8 ctx{ctx}", [ctx] * 8, 64, 8, torch.bfloat16 if dtype != torch.float32 else dtype))
     return cases

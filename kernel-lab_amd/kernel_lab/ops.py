@@ -21,6 +21,9 @@ import torch
 
 from kernel_lab import _native
 
+# num_splits value asking for the device-balanced schedule (KL_SPLITS_BALANCED).
+BALANCED = -1
+
 SUPPORTED_HEAD_DIMS = (16, 32, 64, 128, 256)
 
 
@@ -122,7 +125,9 @@ def paged_decode_attention(
 ) -> torch.Tensor:
     """Single-token decode attention over a paged KV cache (NHD layout).
 
-    ``num_splits`` overrides the split planner (``None`` or 0: planner).
+    ``num_splits`` overrides the split planner (``None`` or 0: planner;
+    ``BALANCED`` (-1): pages of all sequences cut into equal per-workgroup
+    ranges on the device, for batches of very uneven lengths).
     ``max_seq_len`` bounds the work per sequence; without it the block table's
     width is used, so ``seq_lens`` is never read back to the host.
     """

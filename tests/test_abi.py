@@ -110,6 +110,19 @@ def test_planner_balances_when_units_do_not_fill_the_device(batch, hkv, max_page
         assert splits == 1 and ws == 0
 
 
+def test_requested_balanced_schedule_at_any_batch():
+    """KL_SPLITS_BALANCED (-1) picks the balanced schedule even when units fill
+    the device; the VALU path (fp32) takes the planner's uniform splits."""
+    splits, ws = ops.plan_decode(torch.float16, 64, 32, 8, 128, 16, 256, ops.BALANCED, 256)
+    units = 64 * 8
+    assert splits == 0 and ws >= (units + units) * 4 * (128 + 1) * 4
+    assert ops.plan_decode(torch.float32, 64, 32, 8, 128, 16, 256, ops.BALANCED, 256) == ops.plan_decode(
+        torch.float32, 64, 32, 8, 128, 16, 256, 0, 256
+    )
+    with pytest.raises(ValueError):
+        ops.plan_decode(torch.float16, 2, 4, 2, 32, 16, 4, -2)
+
+
 @pytest.mark.parametrize(("requested", "max_pages", "want"), [(1, 5, 1), (2, 5, 2), (3, 5, 3), (5, 5, 5), (64, 5, 5), (4, 7, 4), (5, 7, 4)])
 def test_requested_splits_normalise_like_the_original(requested, max_pages, want):
     """pages_per_split = cdiv(max_pages, S); S = cdiv(max_pages, pages_per_split)

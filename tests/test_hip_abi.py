@@ -42,7 +42,7 @@ def test_rms_norm_through_c_abi(gpu_ops, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("num_splits", [0, 1, 5])
+@pytest.mark.parametrize("num_splits", [0, 1, 5, -1])
 def test_decode_through_c_abi(gpu_ops, dtype, num_splits):
     lib = _native.core()
     q, kv, _, _ = random_decode_problem([7, 300, 33], 32, 8, 128, 16, dtype=dtype, device="cuda", poison=float("nan"))
@@ -57,7 +57,7 @@ def test_decode_through_c_abi(gpu_ops, dtype, num_splits):
     workspace = torch.empty(max(ws.value, 1), dtype=torch.uint8, device="cuda")
     out = torch.empty_like(q)
     args = [code, out.data_ptr(), q.data_ptr(), kv.k_cache.data_ptr(), kv.v_cache.data_ptr(), kv.block_table.data_ptr(),
-            kv.seq_lens.data_ptr(), batch, hq, hkv, d, p, kv.block_table.stride(0), max_pages, d**-0.5, splits.value]
+            kv.seq_lens.data_ptr(), batch, hq, hkv, d, p, kv.block_table.stride(0), max_pages, d**-0.5, num_splits]
     if ws.value:
         # Too small a workspace is refused before anything launches.
         assert lib.kl_paged_decode_attention(*args, workspace.data_ptr(), ws.value - 1, stream_handle()) == 3
@@ -99,3 +99,30 @@ def test_ops_work_under_torch_compile(gpu_ops):
     ref_y, ref_r = ref.fused_add_rms_norm(x.cpu(), r0.cpu(), w.cpu())
     assert torch.equal(r_new.cpu(), ref_r)
     torch.testing.assert_close(y.cpu(), ref_y, **tolerance(torch.float16))
+
+
+def test_balanced_request_reaches_the_planner_on_full_batches(gpu_ops):
+    """64 sequences x 8 KV heads fill the device, so the planner's own choice is
+    one uniform split (no workspace); KL_SPLITS_BALANCED (-1) still gets the
+    balanced schedule, which needs a workspace and is refused without one."""
+    lib = _native.core()
+    lens = [4000] + [100] * 63
+    q, kv, _, _ = random_decode_problem(lens, 32, 8, 128, 16, dtype=torch.float16, device="cuda", poison=float("nan"))
+    batch, hq, d = q.shape
+    max_pages = kv.block_table.shape[1]
+    code = _native.DTYPE_CODES[torch.float16]
+    sizes = {}
+    for req in (0, -1):
+        splits, ws = ctypes.c_int(0), ctypes.c_size_t(0)
+        assert lib.kl_paged_decode_plan(code, batch, hq, 8, d, 16, max_pages, req, 0, ctypes.byref(splits), ctypes.byref(ws)) == 0
+        sizes[req] = (splits.value, ws.value)
+    assert sizes[0] == (1, 0) and sizes[-1][0] == 0 and sizes[-1][1] > 0
+    out = torch.empty_like(q)
+    args = [code, out.data_ptr(), q.data_ptr(), kv.k_cache.data_ptr(), kv.v_cache.data_ptr(), kv.block_table.data_ptr(),
+            kv.seq_lens.data_ptr(), batch, hq, 8, d, 16, kv.block_table.stride(0), max_pages, d**-0.5, -1]
+    assert lib.kl_paged_decode_attention(*args, None, 0, stream_handle()) == 3
+    workspace = torch.empty(sizes[-1][1], dtype=torch.uint8, device="cuda")
+    assert lib.kl_paged_decode_attention(*args, workspace.data_ptr(), sizes[-1][1], stream_handle()) == 0
+    torch.cuda.synchronize()
+    want = ref.paged_decode_attention(q.cpu(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table.cpu(), kv.seq_lens.cpu())
+    torch.testing.assert_close(out.cpu(), want, **tolerance(torch.float16))

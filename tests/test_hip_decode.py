@@ -282,3 +282,36 @@ def test_planner_and_uniform_splits_agree(gpu_ops):
     a = run(gpu_ops, q.half(), type(kv)(kv.k_cache.half(), kv.v_cache.half(), kv.block_table, kv.seq_lens, 16))
     b = run(gpu_ops, q.half(), type(kv)(kv.k_cache.half(), kv.v_cache.half(), kv.block_table, kv.seq_lens, 16), num_splits=7)
     torch.testing.assert_close(a.float().cpu(), b.float().cpu(), atol=2e-3, rtol=2e-3)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_balanced_schedule_over_64_sequences(gpu_ops, dtype):
+    """More sequences than lanes in a wave: the schedule scans seq_lens in
+    64-sequence chunks (planner path, MQA so units stay under the CU count)."""
+    g = torch.Generator().manual_seed(12)
+    lens = torch.randint(1, 1500, (150,), generator=g).tolist()
+    lens[3] = 4000
+    q, kv, _, _ = random_decode_problem(lens, 8, 1, 128, 16, dtype=dtype, device="cuda", poison=float("nan"))
+    kv.seq_lens[70] = 0
+    kv.seq_lens[149] = 0
+    out = run(gpu_ops, q, kv)
+    assert torch.equal(out[70].cpu(), torch.zeros_like(out[70].cpu()))
+    keep = [i for i in range(150) if i not in (70, 149)]
+    sub = type(kv)(kv.k_cache, kv.v_cache, kv.block_table[keep], kv.seq_lens[keep], 16)
+    check(out[keep], expected(q[keep], sub), dtype)
+
+
+@pytest.mark.parametrize(("lens", "hq", "hkv"), [([9000] + [700] * 69, 32, 8), ([1] * 40 + [3000] * 3, 64, 8)])
+def test_requested_balanced_schedule_on_full_batches(gpu_ops, lens, hq, hkv):
+    """num_splits=BALANCED with more (sequence, KV head) units than CUs."""
+    from kernel_lab import ops
+
+    q, kv, _, _ = random_decode_problem(lens, hq, hkv, 128, 16, dtype=torch.float16, device="cuda", poison=float("nan"))
+    check(run(gpu_ops, q, kv, num_splits=ops.BALANCED), expected(q, kv), torch.float16)
+
+
+def test_requested_balanced_schedule_falls_back_for_fp32(gpu_ops):
+    from kernel_lab import ops
+
+    q, kv, _, _ = random_decode_problem([300, 20], 8, 2, 64, 16, dtype=torch.float32, device="cuda")
+    check(run(gpu_ops, q, kv, num_splits=ops.BALANCED), expected(q, kv), torch.float32)
