@@ -6,24 +6,33 @@
 // (the math). Drop-in boundary: csrc/paged_attention.cu:180-199 and
 // csrc/kernel_lab.h:21-33.
 //
-// Work unit: (sequence b, KV head, head group, split). A split owns a range of
-// `pages_per_split` pages of its sequence. Its workgroup has four waves; the
-// unit's 16-token blocks go round-robin to the waves, each wave keeps its own
-// running max / normaliser / output, and the waves merge through LDS at the
-// end. With one split the workgroup writes the final output; otherwise it
-// writes an fp32 partial output and its log2-sum-exp, and a merge kernel
-// combines the splits of each (sequence, query head).
+// Work unit: (sequence b, KV head, head group) and a range of its pages. Two
+// schedules cut the units into workgroup segments:
+//   uniform splits   a split owns `pages_per_split` pages of every unit (the
+//                    original project's rule); one workgroup per (unit, split);
+//   balanced         the pages of all units are laid end to end and cut into
+//                    equal per-workgroup ranges on the device from seq_lens, so
+//                    a long sequence among short ones is spread over many
+//                    workgroups (chosen when units do not fill the device, or
+//                    on request).
+// A workgroup has four waves; a segment's 16-token blocks go round-robin to
+// the waves, each wave keeps its own running max / normaliser / output, and
+// the waves merge through LDS at the end. A segment that covers its whole unit
+// writes the final output; otherwise it writes an fp32 partial output and its
+// log2-sum-exp, and a merge kernel combines the partials of each (sequence,
+// query head).
 //
 // MFMA path (fp16 / bf16, page_size % 16 == 0, head_dim in {32,64,128,256}):
 //   S  = K . Q^T    v_mfma_f32_16x16x32_{f16,bf16}: rows = 16 tokens of a
 //                   block, columns = up to 16 query heads of the GQA group.
-//                   K goes from HBM straight into the A operand (lane = token,
-//                   8 consecutive head dims per lane, 16-byte loads).
+//                   K is loaded row-coalesced (16 lanes read one token's head
+//                   dims), restaged through a per-wave LDS tile and read back
+//                   as the A operand (lane = token, 8 consecutive head dims).
 //   O^T += V^T P^T  v_mfma_f32_16x16x16_{f16,bf16}: the score tile's output
 //                   layout (lane = head, 4 consecutive tokens) is exactly the
 //                   B operand layout, so P never leaves registers. V is loaded
-//                   with fully coalesced 16-byte loads, staged in a per-wave
-//                   LDS tile and read back transposed as the A operand.
+//                   the same row-coalesced way, staged in LDS and read back
+//                   transposed (ds_read_b64_tr_b16) as the A operand.
 // Every K/V element is read from HBM once per unit and used by the whole GQA
 // group. Tokens past seq_len inside the last page are excluded by selects
 // (scores to -inf, V rows to zero), never by multiplying by zero, so NaN or
