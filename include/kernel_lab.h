@@ -130,6 +130,30 @@ int kl_paged_decode_attention(kl_dtype dtype, void* out, const void* q, const vo
                               int num_splits, void* workspace, size_t workspace_bytes,
                               kl_stream_t stream);
 
+/*
+ * Paged decode over an FP8 KV cache: k_cache / v_cache hold OCP FP8 E4M3
+ * codes ("e4m3fn": bias 7, no infinities, 0x7f / 0xff are NaN), one byte per
+ * element, in the same [num_pages, page_size, num_kv_heads, head_dim] layout;
+ * head h's values are k_scale[h] * decode(k) and v_scale[h] * decode(v)
+ * (k_scale, v_scale: [num_kv_heads] fp32 device arrays). q and out are fp16
+ * or bf16 (`dtype`); the cache values are decoded exactly to that type, so
+ * the arithmetic is that of kl_paged_decode_attention.
+ *
+ * Reference counterpart: none in the shipped kernels; the original project
+ * names an FP8 KV cache as planned work (README.md:98). Arguments, workspace
+ * (size it with kl_paged_decode_plan for the same dtype and shape) and status
+ * codes are those of kl_paged_decode_attention; head_dim must be 64, 128 or
+ * 256 and page_size a multiple of 16 (KL_ERR_UNSUPPORTED otherwise).
+ */
+int kl_paged_decode_attention_fp8(kl_dtype dtype, void* out, const void* q,
+                                  const void* k_cache, const void* v_cache,
+                                  const float* k_scale, const float* v_scale,
+                                  const int32_t* block_table, const int32_t* seq_lens,
+                                  int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                  int page_size, int64_t block_table_stride, int max_pages,
+                                  float scale, int num_splits, void* workspace,
+                                  size_t workspace_bytes, kl_stream_t stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

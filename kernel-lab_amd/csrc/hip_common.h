@@ -11,6 +11,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace kl {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -56,6 +58,35 @@ struct BF16 {
     return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
   }
 };
+
+// OCP FP8 E4M3 ("e4m3fn": bias 7, no infinities, NaN = S.1111.111), a storage
+// format only: values are decoded before any arithmetic.
+struct Fp8E4M3 {
+  using S = uint8_t;
+  static constexpr int kBytes = 1;
+};
+
+// Two e4m3 codes (bytes 0-1, or 2-3 when HI, of w) decoded to a packed pair of
+// E (fp16 or bf16), first code in the low half. Every e4m3 value, NaN and the
+// signed zeros included, is exact in both types; gfx950's conversion was
+// checked against all 256 codes. The scale operand is 1: the caller applies
+// its own per-head scales outside the inner loop.
+template <typename E, bool HI>
+__device__ __forceinline__ uint32_t fp8x2_to(uint32_t w) {
+  if constexpr (std::is_same_v<E, BF16>) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI));
+  } else {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, HI));
+  }
+}
+
+// Sixteen e4m3 codes (one 16-byte load) decoded to sixteen E values, codes
+// 0-7 in lo and 8-15 in hi, memory order kept.
+template <typename E>
+__device__ __forceinline__ void fp8x16_to(u32x4 w, u32x4& lo, u32x4& hi) {
+  lo = u32x4{fp8x2_to<E, false>(w[0]), fp8x2_to<E, true>(w[0]), fp8x2_to<E, false>(w[1]), fp8x2_to<E, true>(w[1])};
+  hi = u32x4{fp8x2_to<E, false>(w[2]), fp8x2_to<E, true>(w[2]), fp8x2_to<E, false>(w[3]), fp8x2_to<E, true>(w[3])};
+}
 
 // Low / high 16-bit halves of a 32-bit word as floats (fp16 or bf16 storage).
 template <typename E>
@@ -192,8 +223,12 @@ __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane
 // constant space a uniform address becomes a scalar load. Only for memory no
 // kernel of the launch writes.
 typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
+typedef const __attribute__((address_space(4))) float* const_f32_ptr;
 __device__ __forceinline__ const_i32_ptr as_constant(const int32_t* p) {
   return (const_i32_ptr)(p);
+}
+__device__ __forceinline__ const_f32_ptr as_constant(const float* p) {
+  return (const_f32_ptr)(p);
 }
 
 }  // namespace kl

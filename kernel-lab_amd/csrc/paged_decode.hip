@@ -90,6 +90,8 @@ struct DecodeArgs {
   void* out;
   const int32_t* block_table;
   const int32_t* seq_lens;
+  const float* k_scale;  // [num_kv_heads] dequantisation scales of an FP8 cache; null otherwise
+  const float* v_scale;
   float* o_part;    // [batch, num_q_heads, num_splits, head_dim]
   float* lse_part;  // [batch, num_q_heads, num_splits], log2 domain
   int64_t bt_stride;
@@ -195,12 +197,14 @@ struct MfmaLds {
 };
 
 // Register pipeline depth: blocks whose K and V are held in VGPRs at once
-// (one being processed, the rest in flight); 8 KiB per block at D = 128.
-// Measured on MI355X at D = 128: 2 stages beat 3..6 (more bytes in flight
-// per wave past ~16 KiB lowers HBM throughput for this access pattern).
-template <int D, int NT>
+// (one being processed, the rest in flight); 8 KiB per block at D = 128 with
+// a 16-bit cache. Measured on MI355X at D = 128: 2 stages beat 3..6 (more
+// bytes in flight per wave past ~16 KiB lowers HBM throughput for this access
+// pattern). An FP8 cache holds half the bytes per block.
+template <int D, int NT, int KB>
 constexpr int mfma_stages() {
   if (KL_DECODE_STAGES > 0) return KL_DECODE_STAGES;
+  if (KB == 1) return D <= 64 ? 8 : D == 128 ? (NT == 2 ? 3 : 4) : 2;
   return D <= 64 ? 6 : 2;
 }
 
@@ -231,17 +235,29 @@ struct Dest {
 // workgroup. Contains two workgroup barriers, reached by every wave; on
 // return only wave 0 may still be writing the result, so a caller that runs
 // another segment must pass a barrier before touching `lds` again.
-template <typename E, int D, int NT>
+//
+// KVF is the cache's element format: E itself, or Fp8E4M3, whose codes are
+// decoded exactly to E while they are staged into LDS; from there on both
+// formats share every instruction. An FP8 cache's per-head scales are folded
+// into the score scale (K) and the epilogue (V): q.(s_k k) = s_k (q.k) and
+// sum p (s_v v) = s_v sum p v.
+template <typename E, typename KVF, int D, int NT>
 __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, const Unit& u, const Dest& dst) {
   using S = typename E::S;
+  using KS = typename KVF::S;          // cache storage type
   using M = Mfma<E>;
-  constexpr int KC = D / 32;           // QK k-chunks; also 16-byte K and V loads per lane per block
+  constexpr bool KV8 = std::is_same_v<KVF, Fp8E4M3>;
+  constexpr int KB = KVF::kBytes;      // cache bytes per element
+  constexpr int KC = D / 32;           // QK k-chunks
   constexpr int DT = D / 16;           // PV output tiles along head_dim
-  constexpr int LPT = D / 8;           // lanes per token row in the V load
-  constexpr int TPL = 64 / LPT;        // tokens per V load instruction
+  constexpr int EPL = 16 / KB;         // cache elements per 16-byte lane load
+  constexpr int LPT = D / EPL;         // lanes per token row in a load
+  constexpr int TPL = 64 / LPT;        // tokens per load instruction
+  constexpr int NL = kBlock / TPL;     // 16-byte loads per lane per block, each of K and V
+  static_assert(TPL <= kBlock && kBlock % TPL == 0, "a load must stay inside its 16-token block");
   constexpr int KROW = MfmaLds<D, NT>::kKRow;
   constexpr int VROW = MfmaLds<D, NT>::kVRow;
-  constexpr int NS = mfma_stages<D, NT>();
+  constexpr int NS = mfma_stages<D, NT, KB>();
 
   const int lane = __lane_id();
   const int wave = wave_id();
@@ -277,8 +293,15 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
     for (int d = 0; d < DT; ++d) acc[t][d] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
 
-  const S* kc = static_cast<const S*>(a.k);
-  const S* vc = static_cast<const S*>(a.v);
+  const KS* kc = static_cast<const KS*>(a.k);
+  const KS* vc = static_cast<const KS*>(a.v);
+  // Score scale (log2 domain) and output scale of this KV head.
+  float qk_scale = a.scale_log2;
+  float out_scale = 1.0f;
+  if constexpr (KV8) {
+    qk_scale *= as_constant(a.k_scale)[u.kvh];
+    out_scale = as_constant(a.v_scale)[u.kvh];
+  }
   const const_i32_ptr bt = as_constant(a.block_table + static_cast<int64_t>(u.b) * a.bt_stride);
   const int bpp = a.page_size / kBlock;  // blocks per page
   const int blk_begin = u.page_begin * bpp;
@@ -289,14 +312,14 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
 
   // Per-lane byte offsets inside a block (token row x head dims), for buffer
   // loads off a per-block wave-uniform base. Load c covers tokens
-  // c*TPL .. c*TPL + TPL-1; lane l reads 16 bytes of token c*TPL + l/LPT.
-  uint32_t k_off[KC], v_off[KC];
+  // c*TPL .. c*TPL + TPL-1; lane l reads 16 bytes (EPL elements) of token
+  // c*TPL + l/LPT, head dims v_dim .. v_dim + EPL - 1.
+  uint32_t kv_off[NL];
   const int v_tok = lane / LPT;
-  const int v_dim = 8 * (lane % LPT);
+  const int v_dim = EPL * (lane % LPT);
 #pragma unroll
-  for (int c = 0; c < KC; ++c) {
-    k_off[c] = static_cast<uint32_t>(((c * TPL + v_tok) * a.token_stride + v_dim) * static_cast<int>(sizeof(S)));
-    v_off[c] = static_cast<uint32_t>(((c * TPL + v_tok) * a.token_stride + v_dim) * static_cast<int>(sizeof(S)));
+  for (int c = 0; c < NL; ++c) {
+    kv_off[c] = static_cast<uint32_t>(((c * TPL + v_tok) * a.token_stride + v_dim) * KB);
   }
   // K and V are both loaded row-coalesced (each 16-lane row reads 256
   // contiguous bytes: a token's head dims), which the memory system streams
@@ -318,31 +341,41 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
            static_cast<int64_t>((blk - pidx * bpp) * kBlock) * a.token_stride + static_cast<int64_t>(u.kvh) * D;
   };
 
-  auto load_k = [&](int64_t base, u32x4 (&kf)[KC]) {
+  auto load_k = [&](int64_t base, u32x4 (&kf)[NL]) {
     const auto kr = make_rsrc(kc + base);
 #pragma unroll
-    for (int c = 0; c < KC; ++c) kf[c] = buffer_load16<kCachePolicyNT>(kr, k_off[c]);
+    for (int c = 0; c < NL; ++c) kf[c] = buffer_load16<kCachePolicyNT>(kr, kv_off[c]);
   };
-  auto load_v = [&](int64_t base, u32x4 (&vf)[KC]) {
+  auto load_v = [&](int64_t base, u32x4 (&vf)[NL]) {
     const auto vr = make_rsrc(vc + base);
 #pragma unroll
-    for (int c = 0; c < KC; ++c) vf[c] = buffer_load16<kCachePolicyNT>(vr, v_off[c]);
+    for (int c = 0; c < NL; ++c) vf[c] = buffer_load16<kCachePolicyNT>(vr, kv_off[c]);
   };
-  auto load_block = [&](int64_t base, u32x4 (&kf)[KC], u32x4 (&vf)[KC]) {
+  auto load_block = [&](int64_t base, u32x4 (&kf)[NL], u32x4 (&vf)[NL]) {
     load_k(base, kf);
     load_v(base, vf);
   };
+  // One 16-byte load's elements into a staging row as E: a plain store for a
+  // 16-bit cache, decoded to two 16-byte chunks for FP8.
+  auto stage16 = [&](S* dst, u32x4 v) {
+    if constexpr (KV8) {
+      u32x4 lo, hi;
+      fp8x16_to<E>(v, lo, hi);
+      *reinterpret_cast<u32x4*>(dst) = lo;
+      *reinterpret_cast<u32x4*>(dst + 8) = hi;
+    } else {
+      *reinterpret_cast<u32x4*>(dst) = v;
+    }
+  };
 
-  auto process_block = [&](int i, const u32x4 (&kf)[KC], const u32x4 (&vf)[KC], auto&& mid) {
+  auto process_block = [&](int i, const u32x4 (&kf)[NL], const u32x4 (&vf)[NL], auto&& mid) {
     // Valid tokens in the block: >= 16 means all; <= 0 only for the padding
     // slots of the last pipeline round (i >= nblk).
     const int nvalid = i < nblk ? u.seq_len - (first + kWaves * i) * kBlock : 0;
 
     // Stage K (its rows past seq_len only feed scores replaced by -inf below).
 #pragma unroll
-    for (int c = 0; c < KC; ++c) {
-      *reinterpret_cast<u32x4*>(kstage + (c * TPL + v_tok) * KROW + v_dim) = kf[c];
-    }
+    for (int c = 0; c < NL; ++c) stage16(kstage + (c * TPL + v_tok) * KROW + v_dim, kf[c]);
     // K as the A operand of S = K Q^T: lane holds token `row`, dims 32c + 8grp .. +7.
     u32x4 ka[KC];
 #pragma unroll
@@ -359,7 +392,7 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
       for (int c = 0; c < KC; ++c) s = M::qk(ka[c], qf[t][c], s);
       float sc[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) sc[j] = (4 * grp + j < nvalid) ? s[j] * a.scale_log2 : -INFINITY;
+      for (int j = 0; j < 4; ++j) sc[j] = (4 * grp + j < nvalid) ? s[j] * qk_scale : -INFINITY;
       float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
       mx = max_xor32(max_xor16(mx));
       // A real block's token 0 is valid, so mx is finite; a padding slot has
@@ -388,9 +421,9 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
     mid();
     // Stage V, rows past seq_len as zeros, for the transposed reads.
 #pragma unroll
-    for (int c = 0; c < KC; ++c) {
+    for (int c = 0; c < NL; ++c) {
       const int tok = c * TPL + v_tok;
-      *reinterpret_cast<u32x4*>(stage + tok * VROW + v_dim) = tok < nvalid ? vf[c] : u32x4{0, 0, 0, 0};
+      stage16(stage + tok * VROW + v_dim, tok < nvalid ? vf[c] : u32x4{0, 0, 0, 0});
     }
     // V^T as the A operand: lane holds V[token 4grp + j][dim 16dt + row].
 #pragma unroll
@@ -407,7 +440,7 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
     // branch inside, so the compiler's load-wait counts stay exact; slots past
     // the last block re-read the last block (cache-resident) and process it
     // with no valid token, which leaves the running state unchanged.
-    u32x4 kb[NS][KC], vb[NS][KC];
+    u32x4 kb[NS][NL], vb[NS][NL];
     int64_t next_base = block_base(0);
 #pragma unroll
     for (int s = 0; s < NS - 1; ++s) {
@@ -492,7 +525,7 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
         for (int w = 1; w < kWaves; ++w) {
           num += lds_acc[((((w - 1) * NT + t) * DT + dt) * 4 + i) * 64 + lane] * cw[w];
         }
-        o[i] = num / denom;
+        o[i] = num / denom * out_scale;
       }
       if (!valid) continue;
       const int d = 16 * dt + 4 * grp;
@@ -510,7 +543,7 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
 
 // Uniform splits: workgroup = (sequence, KV head, head group, split), the
 // split owning pages_per_split pages (the reference's decomposition).
-template <typename E, int D, int NT>
+template <typename E, typename KVF, int D, int NT>
 __global__ void __launch_bounds__(kThreads, (mfma_waves_per_eu<D, NT>())) decode_mfma_kernel(const DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[MfmaLds<D, NT>::kBytes];
   const Unit u = decode_unit(a);
@@ -525,7 +558,7 @@ __global__ void __launch_bounds__(kThreads, (mfma_waves_per_eu<D, NT>())) decode
   dst.lse = dst.final ? nullptr : a.lse_part + head0 * a.num_splits + u.split;
   dst.o_head_stride = static_cast<int64_t>(a.num_splits) * D;
   dst.lse_head_stride = a.num_splits;
-  mfma_segment<E, D, NT>(a, lds, u, dst);
+  mfma_segment<E, KVF, D, NT>(a, lds, u, dst);
 }
 
 // ------------------------------------------------------- balanced schedule
@@ -649,7 +682,7 @@ __device__ __forceinline__ Start schedule_start(const DecodeArgs& a, int units_p
   return s;
 }
 
-template <typename E, int D, int NT>
+template <typename E, typename KVF, int D, int NT>
 __global__ void __launch_bounds__(kThreads, (mfma_waves_per_eu<D, NT>()))
     decode_mfma_balanced_kernel(const DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[MfmaLds<D, NT>::kBytes];
@@ -691,7 +724,7 @@ __global__ void __launch_bounds__(kThreads, (mfma_waves_per_eu<D, NT>()))
     dst.lse_head_stride = 1;
 
     __syncthreads();  // the previous segment's wave 0 may still read LDS
-    mfma_segment<E, D, NT>(a, lds, u, dst);
+    mfma_segment<E, KVF, D, NT>(a, lds, u, dst);
 
     pos = unit_base + page1;
     if (r == hp - 1 && page1 == n) {  // this sequence's units are done: next non-empty one
@@ -1103,31 +1136,37 @@ int make_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads, int 
   return ok();
 }
 
-template <typename E>
-int launch_split(const DecodeArgs& a, int head_dim, bool mfma, unsigned grid, hipStream_t stream) {
-  if (mfma) {
-    if constexpr (!std::is_same_v<E, F32>) {
-      const bool two = a.heads_per_wg > 16;
-      switch (head_dim) {
-        case 32:
-          two ? decode_mfma_kernel<E, 32, 2><<<grid, kThreads, 0, stream>>>(a)
-              : decode_mfma_kernel<E, 32, 1><<<grid, kThreads, 0, stream>>>(a);
-          return KL_OK;
-        case 64:
-          two ? decode_mfma_kernel<E, 64, 2><<<grid, kThreads, 0, stream>>>(a)
-              : decode_mfma_kernel<E, 64, 1><<<grid, kThreads, 0, stream>>>(a);
-          return KL_OK;
-        case 128:
-          two ? decode_mfma_kernel<E, 128, 2><<<grid, kThreads, 0, stream>>>(a)
-              : decode_mfma_kernel<E, 128, 1><<<grid, kThreads, 0, stream>>>(a);
-          return KL_OK;
-        case 256:
-          decode_mfma_kernel<E, 256, 1><<<grid, kThreads, 0, stream>>>(a);
-          return KL_OK;
-      }
-    }
-    return fail(KL_ERR_UNSUPPORTED, "no MFMA kernel for this head_dim");
+template <int N>
+using IntC = std::integral_constant<int, N>;
+
+// Calls f(IntC<D>, IntC<NT>) for the MFMA kernel instance that serves
+// head_dim and the workgroup's head tiling (NT = 2 for more than 16 query
+// heads per workgroup).
+template <typename F>
+int dispatch_mfma(int head_dim, int heads_per_wg, F&& f) {
+  const bool two = heads_per_wg > 16;
+  switch (head_dim) {
+    case 32:
+      return two ? f(IntC<32>{}, IntC<2>{}) : f(IntC<32>{}, IntC<1>{});
+    case 64:
+      return two ? f(IntC<64>{}, IntC<2>{}) : f(IntC<64>{}, IntC<1>{});
+    case 128:
+      return two ? f(IntC<128>{}, IntC<2>{}) : f(IntC<128>{}, IntC<1>{});
+    case 256:
+      return f(IntC<256>{}, IntC<1>{});
   }
+  return fail(KL_ERR_UNSUPPORTED, "no MFMA kernel for this head_dim");
+}
+
+// FP8 caches need 16-token blocks of at least one full 16-byte load per lane:
+// head_dim >= 64.
+template <typename KVF, int D>
+constexpr bool mfma_instance_exists() {
+  return KVF::kBytes == 2 || D >= 64;
+}
+
+template <typename E>
+int launch_valu(const DecodeArgs& a, int head_dim, unsigned grid, hipStream_t stream) {
 #define KL_VALU_CASE(DIM)                                                                     \
   case DIM:                                                                                   \
     if constexpr (DIM / (16 / E::kBytes) >= 1 && DIM / (16 / E::kBytes) <= 64) {              \
@@ -1158,45 +1197,57 @@ int launch_split(const DecodeArgs& a, int head_dim, bool mfma, unsigned grid, hi
   return fail(KL_ERR_UNSUPPORTED, "no kernel for this head_dim");
 }
 
-template <typename E>
-int launch_balanced(const DecodeArgs& a, int head_dim, hipStream_t stream) {
-  if constexpr (!std::is_same_v<E, F32>) {
-    const unsigned grid = static_cast<unsigned>(a.grid);
-    const bool two = a.heads_per_wg > 16;
-    switch (head_dim) {
-      case 32:
-        two ? decode_mfma_balanced_kernel<E, 32, 2><<<grid, kThreads, 0, stream>>>(a)
-            : decode_mfma_balanced_kernel<E, 32, 1><<<grid, kThreads, 0, stream>>>(a);
-        break;
-      case 64:
-        two ? decode_mfma_balanced_kernel<E, 64, 2><<<grid, kThreads, 0, stream>>>(a)
-            : decode_mfma_balanced_kernel<E, 64, 1><<<grid, kThreads, 0, stream>>>(a);
-        break;
-      case 128:
-        two ? decode_mfma_balanced_kernel<E, 128, 2><<<grid, kThreads, 0, stream>>>(a)
-            : decode_mfma_balanced_kernel<E, 128, 1><<<grid, kThreads, 0, stream>>>(a);
-        break;
-      case 256:
-        decode_mfma_balanced_kernel<E, 256, 1><<<grid, kThreads, 0, stream>>>(a);
-        break;
-      default:
-        return fail(KL_ERR_UNSUPPORTED, "no MFMA kernel for this head_dim");
+template <typename E, typename KVF>
+int launch_uniform_mfma(const DecodeArgs& a, int head_dim, unsigned grid, hipStream_t stream) {
+  return dispatch_mfma(head_dim, a.heads_per_wg, [&](auto d, auto nt) -> int {
+    constexpr int D = decltype(d)::value, NT = decltype(nt)::value;
+    if constexpr (mfma_instance_exists<KVF, D>()) {
+      decode_mfma_kernel<E, KVF, D, NT><<<grid, kThreads, 0, stream>>>(a);
+      return KL_OK;
+    } else {
+      return fail(KL_ERR_UNSUPPORTED, "an FP8 cache needs head_dim 64, 128 or 256");
     }
-    int st = check_launch("paged decode balanced kernel launch");
-    if (st != KL_OK) return st;
-    decode_merge_balanced_kernel<E>
-        <<<static_cast<unsigned>(static_cast<int64_t>(a.batch) * a.num_q_heads), 64, 0, stream>>>(a, head_dim);
-    return check_launch("paged decode balanced merge kernel launch");
-  }
-  return fail(KL_ERR_UNSUPPORTED, "the balanced schedule needs fp16 or bf16");
+  });
 }
 
-template <typename E>
+template <typename E, typename KVF>
+int launch_balanced(const DecodeArgs& a, int head_dim, hipStream_t stream) {
+  const unsigned grid = static_cast<unsigned>(a.grid);
+  int st = dispatch_mfma(head_dim, a.heads_per_wg, [&](auto d, auto nt) -> int {
+    constexpr int D = decltype(d)::value, NT = decltype(nt)::value;
+    if constexpr (mfma_instance_exists<KVF, D>()) {
+      decode_mfma_balanced_kernel<E, KVF, D, NT><<<grid, kThreads, 0, stream>>>(a);
+      return KL_OK;
+    } else {
+      return fail(KL_ERR_UNSUPPORTED, "an FP8 cache needs head_dim 64, 128 or 256");
+    }
+  });
+  if (st != KL_OK) return st;
+  st = check_launch("paged decode balanced kernel launch");
+  if (st != KL_OK) return st;
+  decode_merge_balanced_kernel<E>
+      <<<static_cast<unsigned>(static_cast<int64_t>(a.batch) * a.num_q_heads), 64, 0, stream>>>(a, head_dim);
+  return check_launch("paged decode balanced merge kernel launch");
+}
+
+// E: query / output format; KVF: cache format (E, or Fp8E4M3 on the MFMA path).
+template <typename E, typename KVF>
 int launch_typed(DecodeArgs& a, int head_dim, bool mfma, hipStream_t stream) {
-  if (a.grid > 0) return launch_balanced<E>(a, head_dim, stream);
+  if constexpr (std::is_same_v<E, F32>) {
+    if (mfma || a.grid > 0) return fail(KL_ERR_UNSUPPORTED, "fp32 runs on the VALU path only");
+  }
+  if (a.grid > 0) {
+    if constexpr (!std::is_same_v<E, F32>) return launch_balanced<E, KVF>(a, head_dim, stream);
+  }
   const int64_t wgs = static_cast<int64_t>(a.batch) * a.num_kv_heads * a.head_groups * a.num_splits;
   if (wgs > 0x7fffffffLL) return fail(KL_ERR_UNSUPPORTED, "too many workgroups");
-  int st = launch_split<E>(a, head_dim, mfma, static_cast<unsigned>(wgs), stream);
+  int st;
+  if constexpr (!std::is_same_v<E, F32>) {
+    st = mfma ? launch_uniform_mfma<E, KVF>(a, head_dim, static_cast<unsigned>(wgs), stream)
+              : launch_valu<E>(a, head_dim, static_cast<unsigned>(wgs), stream);
+  } else {
+    st = launch_valu<E>(a, head_dim, static_cast<unsigned>(wgs), stream);
+  }
   if (st != KL_OK) return st;
   st = check_launch("paged decode split kernel launch");
   if (st != KL_OK) return st;
@@ -1225,13 +1276,26 @@ extern "C" int kl_paged_decode_plan(kl_dtype dtype, int batch, int num_q_heads, 
   return ok();
 }
 
-extern "C" int kl_paged_decode_attention(kl_dtype dtype, void* out, const void* q, const void* k_cache,
-                                         const void* v_cache, const int32_t* block_table, const int32_t* seq_lens,
-                                         int batch, int num_q_heads, int num_kv_heads, int head_dim, int page_size,
-                                         int64_t block_table_stride, int max_pages, float scale, int num_splits,
-                                         void* workspace, size_t workspace_bytes, kl_stream_t stream) {
-  using namespace kl;
+namespace kl {
+namespace {
+
+// Shared body of the two decode entry points. kv8: the caches hold OCP e4m3
+// codes with per-KV-head fp32 scales; otherwise they hold `dtype` like q.
+int decode_entry(kl_dtype dtype, bool kv8, void* out, const void* q, const void* k_cache, const void* v_cache,
+                 const float* k_scale, const float* v_scale, const int32_t* block_table, const int32_t* seq_lens,
+                 int batch, int num_q_heads, int num_kv_heads, int head_dim, int page_size,
+                 int64_t block_table_stride, int max_pages, float scale, int num_splits, void* workspace,
+                 size_t workspace_bytes, hipStream_t stream) {
   if (batch == 0) return ok();
+  if (kv8) {
+    if (dtype != KL_DTYPE_F16 && dtype != KL_DTYPE_BF16) {
+      return fail(KL_ERR_UNSUPPORTED, "an FP8 cache needs fp16 or bf16 queries");
+    }
+    if (!mfma_path(dtype, head_dim, page_size) || head_dim < 64) {
+      return fail(KL_ERR_UNSUPPORTED, "an FP8 cache needs head_dim 64, 128 or 256 and page_size a multiple of 16");
+    }
+    if (!k_scale || !v_scale) return fail(KL_ERR_INVALID_ARGUMENT, "k_scale and v_scale must be non-null");
+  }
   Plan p;
   int st = make_plan(dtype, batch, num_q_heads, num_kv_heads, head_dim, page_size, max_pages, num_splits,
                      current_cu_count(), &p);
@@ -1262,6 +1326,8 @@ extern "C" int kl_paged_decode_attention(kl_dtype dtype, void* out, const void* 
   a.out = out;
   a.block_table = block_table;
   a.seq_lens = seq_lens;
+  a.k_scale = kv8 ? k_scale : nullptr;
+  a.v_scale = kv8 ? v_scale : nullptr;
   a.o_part = static_cast<float*>(workspace);
   a.lse_part = workspace ? reinterpret_cast<float*>(static_cast<char*>(workspace) + p.o_bytes) : nullptr;
   a.bt_stride = block_table_stride;
@@ -1283,14 +1349,40 @@ extern "C" int kl_paged_decode_attention(kl_dtype dtype, void* out, const void* 
   a.scale_log2 = scale * kLog2e;
 
   const bool mfma = mfma_path(dtype, head_dim, page_size);
-  const auto s = reinterpret_cast<hipStream_t>(stream);
   switch (dtype) {
     case KL_DTYPE_F32:
-      return launch_typed<F32>(a, head_dim, false, s);
+      return launch_typed<F32, F32>(a, head_dim, false, stream);
     case KL_DTYPE_F16:
-      return launch_typed<F16>(a, head_dim, mfma, s);
+      return kv8 ? launch_typed<F16, Fp8E4M3>(a, head_dim, true, stream)
+                 : launch_typed<F16, F16>(a, head_dim, mfma, stream);
     case KL_DTYPE_BF16:
-      return launch_typed<BF16>(a, head_dim, mfma, s);
+      return kv8 ? launch_typed<BF16, Fp8E4M3>(a, head_dim, true, stream)
+                 : launch_typed<BF16, BF16>(a, head_dim, mfma, stream);
   }
   return fail(KL_ERR_UNSUPPORTED, "dtype must be f32, f16 or bf16");
+}
+
+}  // namespace
+}  // namespace kl
+
+extern "C" int kl_paged_decode_attention(kl_dtype dtype, void* out, const void* q, const void* k_cache,
+                                         const void* v_cache, const int32_t* block_table, const int32_t* seq_lens,
+                                         int batch, int num_q_heads, int num_kv_heads, int head_dim, int page_size,
+                                         int64_t block_table_stride, int max_pages, float scale, int num_splits,
+                                         void* workspace, size_t workspace_bytes, kl_stream_t stream) {
+  return kl::decode_entry(dtype, false, out, q, k_cache, v_cache, nullptr, nullptr, block_table, seq_lens, batch,
+                          num_q_heads, num_kv_heads, head_dim, page_size, block_table_stride, max_pages, scale,
+                          num_splits, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int kl_paged_decode_attention_fp8(kl_dtype dtype, void* out, const void* q, const void* k_cache,
+                                             const void* v_cache, const float* k_scale, const float* v_scale,
+                                             const int32_t* block_table, const int32_t* seq_lens, int batch,
+                                             int num_q_heads, int num_kv_heads, int head_dim, int page_size,
+                                             int64_t block_table_stride, int max_pages, float scale,
+                                             int num_splits, void* workspace, size_t workspace_bytes,
+                                             kl_stream_t stream) {
+  return kl::decode_entry(dtype, true, out, q, k_cache, v_cache, k_scale, v_scale, block_table, seq_lens, batch,
+                          num_q_heads, num_kv_heads, head_dim, page_size, block_table_stride, max_pages, scale,
+                          num_splits, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
 }

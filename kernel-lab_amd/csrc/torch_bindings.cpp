@@ -6,11 +6,17 @@
 //   fused_add_rms_norm(Tensor! out, Tensor x, Tensor! residual, Tensor weight, float eps) -> ()
 //   paged_decode_attention(Tensor! out, Tensor q, Tensor k_cache, Tensor v_cache,
 //                          Tensor block_table, Tensor seq_lens, float scale) -> ()
-// plus `fused_add_rmsnorm` (same schema as fused_add_rms_norm) and the overload
+// plus `fused_add_rmsnorm` (same schema as fused_add_rms_norm), the overload
 // `paged_decode_attention.splits(..., int num_splits, int max_seq_len)` for
 // the split-KV controls of the reference's Triton wrapper
-// (kernel_lab/triton_kernels/paged_attention.py:176-211); 0 means "planner
-// decides" and "block-table width" respectively.
+// (kernel_lab/triton_kernels/paged_attention.py:176-211; 0 means "planner
+// decides" and "block-table width" respectively, num_splits -1 the balanced
+// schedule), and
+//   paged_decode_attention_fp8(Tensor! out, Tensor q, Tensor k_cache, Tensor v_cache,
+//                              Tensor block_table, Tensor seq_lens, float scale,
+//                              Tensor k_scale, Tensor v_scale, int num_splits, int max_seq_len) -> ()
+// for a float8_e4m3fn cache with fp32 per-KV-head scales (the FP8 KV cache the
+// reference lists as planned work, README.md:98).
 //
 // Outputs are caller-allocated ("Tensor!" = mutated in place). The only
 // allocation here is the split-KV workspace, taken from PyTorch's caching
@@ -94,9 +100,11 @@ void fused_add_rms_norm(at::Tensor& out, const at::Tensor& x, at::Tensor& residu
 
 // Same checks as paged_decode_attention in the reference
 // (csrc/torch_bindings.cpp:71-93), plus device agreement and max_seq_len.
+// k_scale / v_scale non-null: the caches hold float8_e4m3fn codes.
 void paged_decode_impl(at::Tensor& out, const at::Tensor& q, const at::Tensor& k_cache, const at::Tensor& v_cache,
                        const at::Tensor& block_table, const at::Tensor& seq_lens, double scale, int64_t num_splits,
-                       int64_t max_seq_len) {
+                       int64_t max_seq_len, const at::Tensor* k_scale = nullptr, const at::Tensor* v_scale = nullptr) {
+  const bool kv8 = k_scale != nullptr;
   TORCH_CHECK(q.is_cuda() && k_cache.is_cuda() && v_cache.is_cuda() && out.is_cuda() && block_table.is_cuda() &&
                   seq_lens.is_cuda(),
               "tensors must be on the GPU");
@@ -114,9 +122,24 @@ void paged_decode_impl(at::Tensor& out, const at::Tensor& q, const at::Tensor& k
   TORCH_CHECK(block_table.dim() == 2 && seq_lens.dim() == 1, "block_table is 2-D and seq_lens 1-D");
   TORCH_CHECK(block_table.stride(-1) == 1 && seq_lens.is_contiguous(),
               "block_table rows and seq_lens must be contiguous");
-  TORCH_CHECK(q.scalar_type() == k_cache.scalar_type() && q.scalar_type() == v_cache.scalar_type() &&
-                  q.scalar_type() == out.scalar_type(),
-              "q, caches and out must share a dtype");
+  if (kv8) {
+    TORCH_CHECK(k_cache.scalar_type() == at::kFloat8_e4m3fn && v_cache.scalar_type() == at::kFloat8_e4m3fn,
+                "an FP8 cache must be float8_e4m3fn");
+    TORCH_CHECK((q.scalar_type() == at::kHalf || q.scalar_type() == at::kBFloat16) &&
+                    q.scalar_type() == out.scalar_type(),
+                "with an FP8 cache, q and out must be float16 or bfloat16 and match");
+    TORCH_CHECK(k_scale->is_cuda() && v_scale->is_cuda() && k_scale->device() == dev && v_scale->device() == dev,
+                "k_scale and v_scale must be on the tensors' device");
+    TORCH_CHECK(k_scale->scalar_type() == at::kFloat && v_scale->scalar_type() == at::kFloat &&
+                    k_scale->is_contiguous() && v_scale->is_contiguous(),
+                "k_scale and v_scale must be contiguous float32");
+    TORCH_CHECK(k_scale->numel() == k_cache.size(2) && v_scale->numel() == k_cache.size(2),
+                "k_scale and v_scale need one value per KV head");
+  } else {
+    TORCH_CHECK(q.scalar_type() == k_cache.scalar_type() && q.scalar_type() == v_cache.scalar_type() &&
+                    q.scalar_type() == out.scalar_type(),
+                "q, caches and out must share a dtype");
+  }
 
   const int batch = static_cast<int>(q.size(0));
   const int num_q_heads = static_cast<int>(q.size(1));
@@ -149,13 +172,22 @@ void paged_decode_impl(at::Tensor& out, const at::Tensor& q, const at::Tensor& k
   if (ws_bytes > 0) {
     workspace = at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
   }
+  void* ws = ws_bytes > 0 ? workspace.data_ptr() : nullptr;
+  if (kv8) {
+    check_status(kl_paged_decode_attention_fp8(
+                     dtype, out.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                     k_scale->data_ptr<float>(), v_scale->data_ptr<float>(), block_table.data_ptr<int32_t>(),
+                     seq_lens.data_ptr<int32_t>(), batch, num_q_heads, num_kv_heads, head_dim, page_size, bt_stride,
+                     static_cast<int>(max_pages), static_cast<float>(scale), static_cast<int>(num_splits), ws,
+                     ws_bytes, current_stream(dev)),
+                 "paged_decode_attention_fp8");
+    return;
+  }
   check_status(kl_paged_decode_attention(dtype, out.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
                                          block_table.data_ptr<int32_t>(), seq_lens.data_ptr<int32_t>(), batch,
                                          num_q_heads, num_kv_heads, head_dim, page_size, bt_stride,
                                          static_cast<int>(max_pages), static_cast<float>(scale),
-                                         static_cast<int>(num_splits), ws_bytes > 0 ? workspace.data_ptr() : nullptr,
-                                         ws_bytes,
-                                         current_stream(dev)),
+                                         static_cast<int>(num_splits), ws, ws_bytes, current_stream(dev)),
                "paged_decode_attention");
 }
 
@@ -172,6 +204,14 @@ void paged_decode_attention_splits(at::Tensor& out, const at::Tensor& q, const a
   paged_decode_impl(out, q, k_cache, v_cache, block_table, seq_lens, scale, num_splits, max_seq_len);
 }
 
+void paged_decode_attention_fp8(at::Tensor& out, const at::Tensor& q, const at::Tensor& k_cache,
+                                const at::Tensor& v_cache, const at::Tensor& block_table, const at::Tensor& seq_lens,
+                                double scale, const at::Tensor& k_scale, const at::Tensor& v_scale,
+                                int64_t num_splits, int64_t max_seq_len) {
+  paged_decode_impl(out, q, k_cache, v_cache, block_table, seq_lens, scale, num_splits, max_seq_len, &k_scale,
+                    &v_scale);
+}
+
 }  // namespace
 
 TORCH_LIBRARY(kernel_lab, m) {
@@ -184,6 +224,10 @@ TORCH_LIBRARY(kernel_lab, m) {
   m.def(
       "paged_decode_attention.splits(Tensor! out, Tensor q, Tensor k_cache, Tensor v_cache, "
       "Tensor block_table, Tensor seq_lens, float scale, int num_splits, int max_seq_len) -> ()");
+  m.def(
+      "paged_decode_attention_fp8(Tensor! out, Tensor q, Tensor k_cache, Tensor v_cache, "
+      "Tensor block_table, Tensor seq_lens, float scale, Tensor k_scale, Tensor v_scale, "
+      "int num_splits=0, int max_seq_len=0) -> ()");
 }
 
 // ROCm tensors carry PyTorch's CUDA dispatch key.
@@ -193,4 +237,5 @@ TORCH_LIBRARY_IMPL(kernel_lab, CUDA, m) {
   m.impl("fused_add_rmsnorm", &fused_add_rms_norm);
   m.impl("paged_decode_attention", &paged_decode_attention);
   m.impl("paged_decode_attention.splits", &paged_decode_attention_splits);
+  m.impl("paged_decode_attention_fp8", &paged_decode_attention_fp8);
 }

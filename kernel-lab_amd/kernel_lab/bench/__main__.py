@@ -10,7 +10,9 @@ the measured configurations):
 * decode: Llama-3-8B GQA (32/8/128/16) at batch {1, 8, 32, 64} x context
   {512, 4096} with the planner and with fixed splits; ragged-length MQA
   (32/1/128, batch 64, L ~ U[1, 8192]); long-context 70B-style GQA
-  (64/8/128, batch 8, contexts 32768 and 131072).
+  (64/8/128, batch 8, contexts 32768 and 131072);
+* decode-fp8: the FP8 (E4M3) cache against a 16-bit cache holding the same
+  values, at the headline, ragged and long-context shapes.
 
 Every implementation is checked against the PyTorch baseline before it is
 timed; a wrong result is reported as such, never as a speed. Timing: HIP
@@ -33,7 +35,7 @@ import torch
 
 from kernel_lab import ops
 from kernel_lab.bench.roofline import GPUPeak, Work, decode_attention_work, lookup, rms_norm_work
-from kernel_lab.kv_cache import device_decode_problem
+from kernel_lab.kv_cache import device_decode_problem, quantize_fp8
 
 DTYPES = {"float16": torch.float16, "bfloat16": torch.bfloat16, "float32": torch.float32}
 
@@ -85,13 +87,14 @@ def measure(
     kernel: str,
     shape: str,
     impls: dict[str, Callable[[], torch.Tensor]],
-    work: Work,
+    work: Work | dict[str, Work],
     peak: GPUPeak | None,
     baseline: str,
     atol: float,
     timer: Callable[[Callable[[], object]], float],
 ) -> list[Row]:
-    expected = impls[baseline]()
+    # A copy: implementations may write into one shared output tensor.
+    expected = impls[baseline]().clone()
     rows: list[Row] = []
     base_us = None
     for name, fn in impls.items():
@@ -105,7 +108,8 @@ def measure(
         except Exception as exc:  # unsupported shape, out of memory
             rows.append(Row(kernel, shape, name, None, None, None, None, None, f"skipped: {exc}"[:120]))
             continue
-        gbps = work.bytes / (us * 1e-6) / 1e9
+        w = work[name] if isinstance(work, dict) else work
+        gbps = w.bytes / (us * 1e-6) / 1e9
         if name == baseline:
             base_us = us
         rows.append(
@@ -238,6 +242,52 @@ def decode_suite(dtype: torch.dtype, peak: GPUPeak | None, timer, splits: list[i
     return rows
 
 
+def decode_fp8_cases() -> list[tuple[str, list[int], int, int, torch.dtype]]:
+    g = torch.Generator().manual_seed(3)
+    ragged = torch.randint(1, 8193, (64,), generator=g).tolist()
+    return [
+        ("32/8/128 b1 ctx4096", [4096], 32, 8, torch.float16),
+        ("32/8/128 b8 ctx4096", [4096] * 8, 32, 8, torch.float16),
+        ("32/8/128 b64 ctx4096", [4096] * 64, 32, 8, torch.float16),
+        ("32/1/128 b64 ragged U[1,8192]", ragged, 32, 1, torch.bfloat16),
+        ("64/8/128 b8 ctx32768", [32768] * 8, 64, 8, torch.bfloat16),
+        ("64/8/128 b8 ctx131072", [131072] * 8, 64, 8, torch.bfloat16),
+    ]
+
+
+def decode_fp8_suite(peak: GPUPeak | None, timer) -> list[Row]:
+    """FP8 (E4M3, per-KV-head scales) cache against the 16-bit cache holding the
+    same values: E4M3 values are exact in fp16/bf16, so both compute the same
+    attention and the rows show what halving the KV bytes buys."""
+    rows: list[Row] = []
+    d, page = 128, 16
+    for label, lens, hq, hkv, dt in decode_fp8_cases():
+        q, kv = device_decode_problem(lens, hq, hkv, d, page, dtype=dt, device="cuda")
+        kv8, ks, vs = quantize_fp8(kv)
+        # The same values in the 16-bit format (exact), scales applied.
+        kv.k_cache.copy_(kv8.k_cache.to(dt) * ks.to(dt)[None, None, :, None])
+        kv.v_cache.copy_(kv8.v_cache.to(dt) * vs.to(dt)[None, None, :, None])
+        scale = d**-0.5
+        out16, out8 = torch.empty_like(q), torch.empty_like(q)
+        a16 = (q, kv.k_cache, kv.v_cache, kv.block_table, kv.seq_lens)
+        a8 = (q, kv8.k_cache, kv8.v_cache, kv8.block_table, kv8.seq_lens)
+        impls: dict[str, Callable[[], torch.Tensor]] = {
+            f"hip {str(dt).split('.')[-1]} cache (same values)": lambda: ops.paged_decode_attention(
+                *a16, scale, out=out16
+            ),
+            "hip fp8 cache (planner)": lambda: ops.paged_decode_attention(*a8, scale, out=out8, k_scale=ks, v_scale=vs),
+        }
+        w16 = decode_attention_work(lens, hq, hkv, d, 2)
+        w8 = decode_attention_work(lens, hq, hkv, d, 2, kv_elem_bytes=1)
+        work = {name: (w8 if "fp8" in name else w16) for name in impls}
+        baseline = next(iter(impls))
+        # Scales rounded to the 16-bit type make the two caches differ by a rounding.
+        rows += measure("paged_decode_fp8", label, impls, work, peak, baseline, 3e-2, timer)
+        del q, kv, kv8, a16, a8, out16, out8, impls
+        torch.cuda.empty_cache()
+    return rows
+
+
 # --------------------------------------------------------------------- report
 
 
@@ -263,7 +313,7 @@ def main(argv: list[str] | None = None) -> int:
     parser = argparse.ArgumentParser(
         prog="python -m kernel_lab.bench", description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter
     )
-    parser.add_argument("suite", choices=["rmsnorm", "decode", "all"])
+    parser.add_argument("suite", choices=["rmsnorm", "decode", "decode-fp8", "all"])
     parser.add_argument("--dtype", choices=list(DTYPES), default="float16")
     parser.add_argument("--peak-gbps", type=float, help="override the spec-sheet DRAM bandwidth")
     parser.add_argument("--compile", action="store_true", help="add the torch.compile RMSNorm baseline")
@@ -296,6 +346,8 @@ def main(argv: list[str] | None = None) -> int:
         rows += rmsnorm_suite(dtype, peak, timer, args.compile)
     if args.suite in ("decode", "all"):
         rows += decode_suite(dtype, peak, timer, args.splits, args.baseline_max_gb * 1e9)
+    if args.suite in ("decode-fp8", "all"):
+        rows += decode_fp8_suite(peak, timer)
 
     header = (
         f"### {name} ({arch}), {args.dtype}\n\nPeak DRAM bandwidth used for %: "

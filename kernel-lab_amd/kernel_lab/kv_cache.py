@@ -185,3 +185,45 @@ def device_decode_problem(
         page_size=page_size,
     )
     return q, kv
+
+
+# Largest finite OCP FP8 E4M3 value.
+FP8_E4M3_MAX = 448.0
+
+
+def used_pages(kv: PagedKV) -> torch.Tensor:
+    """Distinct pool pages that hold some sequence's tokens (spares excluded)."""
+    npages = (kv.seq_lens.to(torch.int64) + kv.page_size - 1) // kv.page_size
+    cols = torch.arange(kv.max_pages, device=kv.block_table.device)[None, :] < npages[:, None]
+    return torch.unique(kv.block_table[cols].to(torch.int64))
+
+
+def _head_amax(cache: torch.Tensor, pages: torch.Tensor, chunk: int = 4096) -> torch.Tensor:
+    amax = torch.zeros(cache.shape[2], dtype=torch.float32, device=cache.device)
+    for i in range(0, pages.numel(), chunk):
+        part = cache.index_select(0, pages[i : i + chunk]).float().abs()
+        amax = torch.maximum(amax, part.amax(dim=(0, 1, 3)))
+    return amax
+
+
+def quantize_fp8(kv: PagedKV) -> tuple[PagedKV, torch.Tensor, torch.Tensor]:
+    """The cache in OCP FP8 E4M3 with one float32 scale per KV head.
+
+    scale_h = max |x| over head h's cached tokens / 448 (spare pages do not
+    count), codes = round-to-nearest-even(x / scale_h) as float8_e4m3fn, so
+    head h's values are scale_h * code. Values outside E4M3's range (poisoned
+    spares) become NaN codes, which a correct kernel never reads.
+    """
+    pages = used_pages(kv)
+    out = []
+    scales = []
+    for cache in (kv.k_cache, kv.v_cache):
+        amax = _head_amax(cache, pages)
+        scale = torch.where(amax > 0, amax / FP8_E4M3_MAX, torch.ones_like(amax))
+        codes = torch.empty(cache.shape, dtype=torch.float8_e4m3fn, device=cache.device)
+        for i in range(0, cache.shape[0], 4096):
+            codes[i : i + 4096] = (cache[i : i + 4096].float() / scale[None, None, :, None]).to(torch.float8_e4m3fn)
+        out.append(codes)
+        scales.append(scale)
+    q8 = PagedKV(out[0], out[1], kv.block_table, kv.seq_lens, kv.page_size)
+    return q8, scales[0], scales[1]

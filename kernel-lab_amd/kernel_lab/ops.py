@@ -122,6 +122,8 @@ def paged_decode_attention(
     num_splits: int | None = None,
     max_seq_len: int | None = None,
     out: torch.Tensor | None = None,
+    k_scale: torch.Tensor | float | None = None,
+    v_scale: torch.Tensor | float | None = None,
 ) -> torch.Tensor:
     """Single-token decode attention over a paged KV cache (NHD layout).
 
@@ -130,6 +132,11 @@ def paged_decode_attention(
     ranges on the device, for batches of very uneven lengths).
     ``max_seq_len`` bounds the work per sequence; without it the block table's
     width is used, so ``seq_lens`` is never read back to the host.
+
+    A ``torch.float8_e4m3fn`` cache holds FP8 codes; ``k_scale`` and
+    ``v_scale`` (one float32 per KV head, or one float for all) give head h's
+    values as ``k_scale[h] * k`` and ``v_scale[h] * v``. q is then float16 or
+    bfloat16 and the output has q's dtype.
     """
     _check_decode(q, k_cache, v_cache)
     _native.require_ops()
@@ -137,6 +144,18 @@ def paged_decode_attention(
     q = q.contiguous()
     if out is None:
         out = torch.empty_like(q)
+    if k_cache.dtype == torch.float8_e4m3fn or v_cache.dtype == torch.float8_e4m3fn:
+        if k_scale is None or v_scale is None:
+            raise ValueError("an FP8 cache needs k_scale and v_scale")
+        hkv = k_cache.shape[2]
+        ks = _head_scales(k_scale, hkv, q.device)
+        vs = _head_scales(v_scale, hkv, q.device)
+        torch.ops.kernel_lab.paged_decode_attention_fp8(
+            out, q, k_cache, v_cache, block_table, seq_lens, scale, ks, vs, int(num_splits or 0), int(max_seq_len or 0)
+        )
+        return out
+    if k_scale is not None or v_scale is not None:
+        raise ValueError("k_scale and v_scale apply to an FP8 (float8_e4m3fn) cache only")
     if num_splits is None and max_seq_len is None:
         torch.ops.kernel_lab.paged_decode_attention(out, q, k_cache, v_cache, block_table, seq_lens, scale)
     else:
@@ -144,6 +163,17 @@ def paged_decode_attention(
             out, q, k_cache, v_cache, block_table, seq_lens, scale, int(num_splits or 0), int(max_seq_len or 0)
         )
     return out
+
+
+def _head_scales(s: torch.Tensor | float, num_kv_heads: int, device: torch.device) -> torch.Tensor:
+    """Per-KV-head float32 scales on the device: a tensor of num_kv_heads
+    values, or one number (or one-element tensor) for every head."""
+    t = torch.as_tensor(s, dtype=torch.float32, device=device).reshape(-1)
+    if t.numel() == 1:
+        t = t.expand(num_kv_heads)
+    if t.numel() != num_kv_heads:
+        raise ValueError(f"expected {num_kv_heads} scales (one per KV head), got {t.numel()}")
+    return t.contiguous()
 
 
 def plan_decode(

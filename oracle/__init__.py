@@ -24,6 +24,12 @@ Pinning (each check is in tests/test_oracle.py):
   vectors; planted mistakes (GQA mapping, scale, length, page order) that the
   golden vectors must reject.
 
+* ``reference.paged_decode_attention_fp8``: the E4M3 widening against
+  ``brute.e4m3_table`` (decoded from the OCP bit layout, all 256 codes); the
+  scale identities (k_scale folds into ``scale``, v_scale multiplies the
+  output); float64 brute force on the dequantised cache; a one-hot known
+  answer in exactly representable E4M3 values.
+
 There are no reference golden files to pin against: the original project's
 tests use seeded random data and the known answers above.
 """

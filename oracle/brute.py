@@ -57,3 +57,22 @@ def decode_f64(
             w = np.exp(scores - scores.max())
             out[b, h] = (w[:, None] * vals).sum(axis=0) / w.sum()
     return out
+
+
+def e4m3_decode(code: int) -> float:
+    """Value of an OCP FP8 E4M3 ("e4m3fn") code, from the bit layout alone:
+    sign bit 7, exponent bits 6-3 (bias 7), mantissa bits 2-0; exponent 0 is
+    subnormal (m/8 * 2^-6); S.1111.111 is NaN; no infinities."""
+    sign = -1.0 if code & 0x80 else 1.0
+    exp = (code >> 3) & 0xF
+    man = code & 0x7
+    if exp == 0xF and man == 0x7:
+        return float("nan")
+    if exp == 0:
+        return sign * (man / 8.0) * 2.0**-6
+    return sign * (1.0 + man / 8.0) * 2.0 ** (exp - 7)
+
+
+def e4m3_table() -> np.ndarray:
+    """Float64 values of all 256 E4M3 codes, indexed by code."""
+    return np.array([e4m3_decode(c) for c in range(256)], dtype=np.float64)

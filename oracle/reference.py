@@ -64,6 +64,31 @@ def paged_decode_attention(
     return out
 
 
+def paged_decode_attention_fp8(
+    q: torch.Tensor,
+    k_codes: torch.Tensor,
+    v_codes: torch.Tensor,
+    block_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    k_scale: torch.Tensor,
+    v_scale: torch.Tensor,
+    scale: float | None = None,
+) -> torch.Tensor:
+    """Decode over an OCP FP8 E4M3 cache (float8_e4m3fn codes, same layout):
+    KV head h's values are k_scale[h] * e4m3(code) and v_scale[h] * e4m3(code),
+    then exactly the float32 math of paged_decode_attention, output in q's dtype.
+
+    The original project lists this cache format as planned work
+    (README.md:98) and ships no implementation, so its definition is the
+    16-bit path's math on the dequantised values.
+    """
+    ks = k_scale.float().cpu().reshape(1, 1, -1, 1)
+    vs = v_scale.float().cpu().reshape(1, 1, -1, 1)
+    k = k_codes.cpu().float() * ks
+    v = v_codes.cpu().float() * vs
+    return paged_decode_attention(q.cpu(), k, v, block_table, seq_lens, scale)
+
+
 def dense_decode_attention(
     q: torch.Tensor, keys: list[torch.Tensor], values: list[torch.Tensor], scale: float | None = None
 ) -> torch.Tensor:

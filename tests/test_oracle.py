@@ -60,10 +60,11 @@ def golden_tensors(case: dict[str, np.ndarray], dtype: torch.dtype = torch.float
 
 
 def test_rms_norm_unit_rms_output():
-    """With weight 1 and eps 0 the output has mean square 1 (original tests/test_reference.py:12-15)."""
-    x = torch.randn(8, 512, dtype=torch.float64)
+    """With weight 1 and eps 0 the output has mean square 1 (original tests/test_reference.py:12-15).
+    The oracle computes in float32, so float32 tolerance."""
+    x = torch.randn(8, 512, dtype=torch.float64, generator=torch.Generator().manual_seed(0))
     y = ref.rms_norm(x, torch.ones(512, dtype=torch.float64), eps=0.0)
-    torch.testing.assert_close(y.pow(2).mean(-1), torch.ones(8, dtype=torch.float64))
+    torch.testing.assert_close(y.pow(2).mean(-1), torch.ones(8, dtype=torch.float64), atol=1e-6, rtol=1e-6)
 
 
 def test_rms_norm_matches_torch_builtin():

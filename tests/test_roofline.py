@@ -27,6 +27,13 @@ def test_decode_kv_bytes():
     assert work.flops == 4 * 30 * 4 * 8
 
 
+def test_fp8_cache_halves_the_kv_bytes():
+    w16 = roofline.decode_attention_work([4096] * 64, 32, 8, 128, 2)
+    w8 = roofline.decode_attention_work([4096] * 64, 32, 8, 128, 2, kv_elem_bytes=1)
+    q_out = 2 * 64 * 32 * 128 * 2
+    assert w8.bytes - q_out == (w16.bytes - q_out) // 2 and w8.flops == w16.flops
+
+
 def test_baseline_floors():
     """Algorithmic bytes at the headline shapes (8.0 TB/s floors in the build's targets)."""
     rms = roofline.rms_norm_work(4096, 8192, 2, True)
