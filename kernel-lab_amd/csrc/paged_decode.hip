@@ -922,9 +922,46 @@ __global__ void __launch_bounds__(kThreads) decode_valu_kernel(const DecodeArgs 
 
 // --------------------------------------------------------------- split merge
 
+// Merge of n partials (o_w, lse_w), w = 0 .. n-1, into one output head:
+// out[d] = sum_w 2^(lse_w - M) o_w[d] / sum_w 2^(lse_w - M), M = max_w lse_w.
+// o_w[d] is at op[w * o_stride + d], lse_w at lse[w * l_stride]. The loads go
+// out eight partials at a time with clamped indexes (weight 0 past the end),
+// so a many-way merge is not a chain of dependent load latencies.
+template <typename E>
+__device__ __forceinline__ void merge_partials(const float* lse, int64_t l_stride, const float* op,
+                                               int64_t o_stride, int n, int head_dim, typename E::S* out);
+
 __device__ __forceinline__ float wave_max(float v) {
   v = row16_max(v);
   return fmaxf(fmaxf(lane_read(v, 0), lane_read(v, 16)), fmaxf(lane_read(v, 32), lane_read(v, 48)));
+}
+
+template <typename E>
+__device__ __forceinline__ void merge_partials(const float* lse, int64_t l_stride, const float* op,
+                                               int64_t o_stride, int n, int head_dim, typename E::S* out) {
+  constexpr int U = 8;
+  const int lane = __lane_id();
+  float mx = -INFINITY;
+  for (int w = lane; w < n; w += 64) mx = fmaxf(mx, lse[w * l_stride]);
+  mx = wave_max(mx);
+  float den = 0.0f;
+  for (int w = lane; w < n; w += 64) den += exp2f(lse[w * l_stride] - mx);
+  den = wave_sum(den);
+  for (int d = lane; d < head_dim; d += 64) {
+    float num = 0.0f;
+    for (int w0 = 0; w0 < n; w0 += U) {
+      float wt[U], v[U];
+#pragma unroll
+      for (int j = 0; j < U; ++j) {
+        const int w = min(w0 + j, n - 1);
+        wt[j] = lse[w * l_stride];
+        v[j] = op[w * o_stride + d];
+      }
+#pragma unroll
+      for (int j = 0; j < U; ++j) num += (w0 + j < n ? exp2f(wt[j] - mx) : 0.0f) * v[j];
+    }
+    out[d] = E::from_f32(num / den);
+  }
 }
 
 // out[b, h] = sum_s 2^(lse_s - M) o_s / sum_s 2^(lse_s - M) over the splits that
@@ -949,19 +986,7 @@ __global__ void __launch_bounds__(64) decode_merge_kernel(const DecodeArgs a, in
   }
   const float* lse = a.lse_part + static_cast<int64_t>(bh) * a.num_splits;
   const float* op = a.o_part + static_cast<int64_t>(bh) * a.num_splits * head_dim;
-
-  float mx = -INFINITY;
-  for (int s = lane; s < active; s += 64) mx = fmaxf(mx, lse[s]);
-  mx = wave_max(mx);
-  float den = 0.0f;
-  for (int s = lane; s < active; s += 64) den += exp2f(lse[s] - mx);
-  den = wave_sum(den);
-
-  for (int d = lane; d < head_dim; d += 64) {
-    float num = 0.0f;
-    for (int s = 0; s < active; ++s) num += exp2f(lse[s] - mx) * op[static_cast<int64_t>(s) * head_dim + d];
-    out[d] = E::from_f32(num / den);
-  }
+  merge_partials<E>(lse, 1, op, head_dim, active, head_dim, out);
 }
 
 // Merge for the balanced schedule: one wave per (sequence, query head). Units
@@ -1001,19 +1026,7 @@ __global__ void __launch_bounds__(64) decode_merge_balanced_kernel(const DecodeA
   const int64_t stride_o = static_cast<int64_t>(a.heads_per_wg) * head_dim;
 
   const int nw = static_cast<int>(w1 - w0) + 1;
-  lse += (w0 + uidx) * stride_l;
-  op += (w0 + uidx) * stride_o;
-  float mx = -INFINITY;
-  for (int w = lane; w < nw; w += 64) mx = fmaxf(mx, lse[w * stride_l]);
-  mx = wave_max(mx);
-  float den = 0.0f;
-  for (int w = lane; w < nw; w += 64) den += exp2f(lse[w * stride_l] - mx);
-  den = wave_sum(den);
-  for (int d = lane; d < head_dim; d += 64) {
-    float num = 0.0f;
-    for (int w = 0; w < nw; ++w) num += exp2f(lse[w * stride_l] - mx) * op[w * stride_o + d];
-    out[d] = E::from_f32(num / den);
-  }
+  merge_partials<E>(lse + (w0 + uidx) * stride_l, stride_l, op + (w0 + uidx) * stride_o, stride_o, nw, head_dim, out);
 }
 
 // -------------------------------------------------------------- host side

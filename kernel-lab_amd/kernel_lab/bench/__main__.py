@@ -12,7 +12,9 @@ the measured configurations):
   (32/1/128, batch 64, L ~ U[1, 8192]); long-context 70B-style GQA
   (64/8/128, batch 8, contexts 32768 and 131072);
 * decode-fp8: the FP8 (E4M3) cache against a 16-bit cache holding the same
-  values, at the headline, ragged and long-context shapes.
+  values, at the headline, ragged and long-context shapes;
+* copy: a 1 GiB device copy (the streaming ceiling, and the counter
+  calibration kernel for the profiles).
 
 Every implementation is checked against the PyTorch baseline before it is
 timed; a wrong result is reported as such, never as a speed. Timing: HIP
@@ -214,10 +216,19 @@ def decode_cases(dtype: torch.dtype) -> list[tuple[str, list[int], int, int, tor
     return cases
 
 
-def decode_suite(dtype: torch.dtype, peak: GPUPeak | None, timer, splits: list[int], baseline_max_bytes: float) -> list[Row]:
+def decode_suite(
+    dtype: torch.dtype,
+    peak: GPUPeak | None,
+    timer,
+    splits: list[int],
+    baseline_max_bytes: float,
+    shape: str | None = None,
+) -> list[Row]:
     rows: list[Row] = []
     d, page = 128, 16
     for label, lens, hq, hkv, dt in decode_cases(dtype):
+        if shape and shape not in label:
+            continue
         q, kv = device_decode_problem(lens, hq, hkv, d, page, dtype=dt, device="cuda")
         args = (q, kv.k_cache, kv.v_cache, kv.block_table, kv.seq_lens)
         scale = d**-0.5
@@ -255,13 +266,15 @@ def decode_fp8_cases() -> list[tuple[str, list[int], int, int, torch.dtype]]:
     ]
 
 
-def decode_fp8_suite(peak: GPUPeak | None, timer) -> list[Row]:
+def decode_fp8_suite(peak: GPUPeak | None, timer, shape: str | None = None) -> list[Row]:
     """FP8 (E4M3, per-KV-head scales) cache against the 16-bit cache holding the
     same values: E4M3 values are exact in fp16/bf16, so both compute the same
     attention and the rows show what halving the KV bytes buys."""
     rows: list[Row] = []
     d, page = 128, 16
     for label, lens, hq, hkv, dt in decode_fp8_cases():
+        if shape and shape not in label:
+            continue
         q, kv = device_decode_problem(lens, hq, hkv, d, page, dtype=dt, device="cuda")
         kv8, ks, vs = quantize_fp8(kv)
         # The same values in the 16-bit format (exact), scales applied.
@@ -285,6 +298,23 @@ def decode_fp8_suite(peak: GPUPeak | None, timer) -> list[Row]:
         rows += measure("paged_decode_fp8", label, impls, work, peak, baseline, 3e-2, timer)
         del q, kv, kv8, a16, a8, out16, out8, impls
         torch.cuda.empty_cache()
+    return rows
+
+
+# ------------------------------------------------------------------- copy
+
+
+def copy_suite(peak: GPUPeak | None, timer, mib: int = 1024) -> list[Row]:
+    """A plain device-to-device copy of ``mib`` MiB (torch ``copy_``): the
+    practical streaming ceiling, and the known-size kernel that calibrates the
+    FETCH_SIZE / WRITE_SIZE counters (it reads and writes exactly mib MiB)."""
+    n = mib * (1 << 20) // 4
+    x = torch.ones(n, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    work = Work(bytes=2 * n * 4, flops=0)
+    rows = measure("copy", f"{mib} MiB", {"torch copy_": lambda: y.copy_(x)}, work, peak, "torch copy_", 0.0, timer)
+    del x, y
+    torch.cuda.empty_cache()
     return rows
 
 
@@ -313,7 +343,7 @@ def main(argv: list[str] | None = None) -> int:
     parser = argparse.ArgumentParser(
         prog="python -m kernel_lab.bench", description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter
     )
-    parser.add_argument("suite", choices=["rmsnorm", "decode", "decode-fp8", "all"])
+    parser.add_argument("suite", choices=["rmsnorm", "decode", "decode-fp8", "copy", "all"])
     parser.add_argument("--dtype", choices=list(DTYPES), default="float16")
     parser.add_argument("--peak-gbps", type=float, help="override the spec-sheet DRAM bandwidth")
     parser.add_argument("--compile", action="store_true", help="add the torch.compile RMSNorm baseline")
@@ -322,6 +352,7 @@ def main(argv: list[str] | None = None) -> int:
     parser.add_argument("--flush-mb", type=int, default=1024, help="read this much between timed calls (0: none)")
     parser.add_argument("--baseline-max-gb", type=float, default=8.0, help="skip the gather baseline above this")
     parser.add_argument("--out", type=Path, help="directory for results.json and results.md")
+    parser.add_argument("--shape", help="run only the cases whose shape label contains this text")
     args = parser.parse_args(argv)
 
     if not torch.cuda.is_available():
@@ -345,9 +376,11 @@ def main(argv: list[str] | None = None) -> int:
     if args.suite in ("rmsnorm", "all"):
         rows += rmsnorm_suite(dtype, peak, timer, args.compile)
     if args.suite in ("decode", "all"):
-        rows += decode_suite(dtype, peak, timer, args.splits, args.baseline_max_gb * 1e9)
+        rows += decode_suite(dtype, peak, timer, args.splits, args.baseline_max_gb * 1e9, args.shape)
     if args.suite in ("decode-fp8", "all"):
-        rows += decode_fp8_suite(peak, timer)
+        rows += decode_fp8_suite(peak, timer, args.shape)
+    if args.suite == "copy":
+        rows += copy_suite(peak, timer)
 
     header = (
         f"### {name} ({arch}), {args.dtype}\n\nPeak DRAM bandwidth used for %: "
