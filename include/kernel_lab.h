@@ -154,6 +154,38 @@ int kl_paged_decode_attention_fp8(kl_dtype dtype, void* out, const void* q,
                                   float scale, int num_splits, void* workspace,
                                   size_t workspace_bytes, kl_stream_t stream);
 
+/*
+ * Cascade (shared-prefix) decode: sequence b attends over the prefix_len[0]
+ * tokens of the shared prefix (pages prefix_block_table[0 .. prefix_pages))
+ * followed by its own seq_lens[b] tokens (pages block_table[b, ...]), all in
+ * the same k_cache / v_cache pools. The result is the attention over the
+ * concatenated tokens; a sequence may have no own tokens (seq_lens[b] == 0),
+ * and prefix_pages == 0 makes it plain decode.
+ *
+ * Reference counterpart: none in the shipped kernels; the original project's
+ * design notes name cascade/shared-prefix attention among the decode
+ * features beyond its kernels (docs/design.md:96-100). The prefix's K/V is
+ * streamed once per 32 query heads of the folded batch instead of once per
+ * sequence.
+ *
+ *   prefix_len   device pointer to one int32 (no host sync)
+ *   workspace    at least kl_cascade_decode_plan's bytes, 16-byte aligned
+ *
+ * fp16 / bf16, head_dim 32..256, page_size a multiple of 16; other arguments
+ * and status codes as kl_paged_decode_attention.
+ */
+int kl_cascade_decode_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads,
+                           int head_dim, int page_size, int prefix_pages, int max_pages,
+                           int cu_count, size_t* out_workspace);
+
+int kl_cascade_decode_attention(kl_dtype dtype, void* out, const void* q, const void* k_cache,
+                                const void* v_cache, const int32_t* prefix_block_table,
+                                const int32_t* prefix_len, int prefix_pages,
+                                const int32_t* block_table, const int32_t* seq_lens, int batch,
+                                int num_q_heads, int num_kv_heads, int head_dim, int page_size,
+                                int64_t block_table_stride, int max_pages, float scale,
+                                void* workspace, size_t workspace_bytes, kl_stream_t stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

@@ -109,6 +109,14 @@ struct DecodeArgs {
   int heads_per_wg;     // query heads one workgroup handles
   int grid;             // workgroups of the balanced decode kernel (0: uniform splits)
   float scale_log2;     // scale * log2(e)
+  // Query-row mapping. Local head hl of KV head kvh in sequence b reads q row
+  // (b + hl / q_fold) * q_heads + kvh * q_fold + hl % q_fold, and the output
+  // has q's layout. Plain decode: q_fold = group, q_heads = num_q_heads (the
+  // identity). The shared-prefix pass of cascade decode folds every
+  // sequence's group into one: batch 1, group = B * G, q_fold = G.
+  int q_fold;
+  int q_heads;
+  int force_partial;    // write fp32 partials (o, lse) even with one split
 };
 
 struct Unit {
@@ -218,6 +226,11 @@ constexpr int mfma_waves_per_eu() {
   return NT == 2 ? 2 : 1;
 }
 
+// Row of q (and of the output) that local head hl of unit u reads.
+__device__ __forceinline__ int64_t q_row(const DecodeArgs& a, const Unit& u, int hl) {
+  return static_cast<int64_t>(u.b + hl / a.q_fold) * a.q_heads + u.kvh * a.q_fold + hl % a.q_fold;
+}
+
 // Where a segment's result goes: the normalised output (dtype) when the
 // segment covers its whole unit, else an fp32 partial and its log2-sum-exp.
 // Local head h (0 .. heads_per_wg-1) of the partial lives at o + h*o_head_stride
@@ -274,7 +287,7 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
     for (int t = 0; t < NT; ++t) {
       const int hl = h0 + 16 * t + row;
       const bool valid = hl < a.group;
-      const S* qh = q + (static_cast<int64_t>(u.b) * a.num_q_heads + u.kvh * a.group + (valid ? hl : 0)) * D;
+      const S* qh = q + q_row(a, u, valid ? hl : 0) * D;
 #pragma unroll
       for (int c = 0; c < KC; ++c) {
         const u32x4 v = *reinterpret_cast<const u32x4*>(qh + 32 * c + 8 * grp);
@@ -514,7 +527,7 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
     }
     const int hl = h0 + 16 * t + row;
     const bool valid = hl < a.group;
-    const int64_t head = static_cast<int64_t>(u.b) * a.num_q_heads + u.kvh * a.group + hl;
+    const int64_t head = q_row(a, u, valid ? hl : 0);
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
       float o[4];
@@ -548,11 +561,13 @@ __global__ void __launch_bounds__(kThreads, (mfma_waves_per_eu<D, NT>())) decode
   __shared__ __attribute__((aligned(16))) char lds[MfmaLds<D, NT>::kBytes];
   const Unit u = decode_unit(a);
   if (u.page_begin >= u.page_end) {
-    if (u.split == 0 && u.seq_len <= 0 && a.num_splits == 1) write_zero_heads<typename E::S, E>(a, u, D);
+    if (u.split == 0 && u.seq_len <= 0 && a.num_splits == 1 && !a.force_partial) {
+      write_zero_heads<typename E::S, E>(a, u, D);
+    }
     return;  // a split past the end of its sequence has no work
   }
   Dest dst;
-  dst.final = a.num_splits == 1;
+  dst.final = a.num_splits == 1 && !a.force_partial;
   const int64_t head0 = static_cast<int64_t>(u.b) * a.num_q_heads + u.kvh * a.group + u.hg * a.heads_per_wg;
   dst.o = dst.final ? nullptr : a.o_part + (head0 * a.num_splits + u.split) * D;
   dst.lse = dst.final ? nullptr : a.lse_part + head0 * a.num_splits + u.split;
@@ -1029,6 +1044,93 @@ __global__ void __launch_bounds__(64) decode_merge_balanced_kernel(const DecodeA
   merge_partials<E>(lse + (w0 + uidx) * stride_l, stride_l, op + (w0 + uidx) * stride_o, stride_o, nw, head_dim, out);
 }
 
+// ---------------------------------------------------- cascade (shared prefix)
+//
+// Cascade decode: every sequence attends over a shared prefix (one block-table
+// row of prefix_len tokens) followed by its own tokens. The prefix pass runs
+// the MFMA segment with all sequences' query heads of a KV head folded into
+// one group (q_fold), so each workgroup streams the prefix once for up to 32
+// query rows of many sequences; the suffix pass is the plain split decode.
+// Both write fp32 partials, and this kernel merges them by the LSE rule.
+
+struct CascadeArgs {
+  const float* p_o;          // prefix partials: virtual head kvh*(B*G) + b*G + g, p_splits each
+  const float* p_lse;
+  const int32_t* prefix_len; // device, one value
+  int prefix_pages;          // prefix block-table length
+  int p_splits, p_pps;
+  const float* s_o;          // suffix partials: head b*Hq + h, s_splits each
+  const float* s_lse;
+  const int32_t* seq_lens;
+  int max_pages;
+  int s_splits, s_pps;
+  void* out;
+  int batch, num_q_heads, group, page_size;
+};
+
+// Splits of a pass that hold tokens of a sequence of `len` tokens.
+__device__ __forceinline__ int active_splits(int len, int max_pages, int page_size, int splits, int pps) {
+  const int64_t cap = static_cast<int64_t>(max_pages) * page_size;
+  const int n = static_cast<int>(len < cap ? len : cap);
+  const int pages = n > 0 ? (n + page_size - 1) / page_size : 0;
+  return min(splits, (pages + pps - 1) / pps);
+}
+
+// Adds n partials (o_w at o + w*D, lse_w at lse[w]) to a running
+// sum_w 2^(lse_w - mx) o_w[d], loads issued eight partials at a time.
+__device__ __forceinline__ float merge_accumulate(const float* lse, const float* o, int n, int head_dim, int d,
+                                                  float mx) {
+  constexpr int U = 8;
+  float num = 0.0f;
+  for (int w0 = 0; w0 < n; w0 += U) {
+    float wt[U], v[U];
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      const int w = min(w0 + j, n - 1);
+      wt[j] = lse[w];
+      v[j] = o[static_cast<int64_t>(w) * head_dim + d];
+    }
+#pragma unroll
+    for (int j = 0; j < U; ++j) num += (w0 + j < n ? exp2f(wt[j] - mx) : 0.0f) * v[j];
+  }
+  return num;
+}
+
+template <typename E>
+__global__ void __launch_bounds__(64) cascade_merge_kernel(const CascadeArgs c, int head_dim) {
+  using S = typename E::S;
+  const int lane = __lane_id();
+  const int b = blockIdx.x / c.num_q_heads;
+  const int h = blockIdx.x % c.num_q_heads;
+  const int kvh = h / c.group;
+  const int g = h % c.group;
+  const int np = active_splits(as_constant(c.prefix_len)[0], c.prefix_pages, c.page_size, c.p_splits, c.p_pps);
+  const int ns = active_splits(as_constant(c.seq_lens)[b], c.max_pages, c.page_size, c.s_splits, c.s_pps);
+  const int64_t shead = static_cast<int64_t>(b) * c.num_q_heads + h;
+  S* out = static_cast<S*>(c.out) + shead * head_dim;
+  if (np + ns == 0) {
+    for (int d = lane; d < head_dim; d += 64) out[d] = E::from_f32(0.0f);
+    return;
+  }
+  const int64_t vhead = (static_cast<int64_t>(kvh) * c.batch + b) * c.group + g;
+  const float* pl = c.p_lse + vhead * c.p_splits;
+  const float* po = c.p_o + vhead * c.p_splits * head_dim;
+  const float* sl = c.s_lse + shead * c.s_splits;
+  const float* so = c.s_o + shead * c.s_splits * head_dim;
+  float mx = -INFINITY;
+  for (int w = lane; w < np; w += 64) mx = fmaxf(mx, pl[w]);
+  for (int w = lane; w < ns; w += 64) mx = fmaxf(mx, sl[w]);
+  mx = wave_max(mx);
+  float den = 0.0f;
+  for (int w = lane; w < np; w += 64) den += exp2f(pl[w] - mx);
+  for (int w = lane; w < ns; w += 64) den += exp2f(sl[w] - mx);
+  den = wave_sum(den);
+  for (int d = lane; d < head_dim; d += 64) {
+    const float num = merge_accumulate(pl, po, np, head_dim, d, mx) + merge_accumulate(sl, so, ns, head_dim, d, mx);
+    out[d] = E::from_f32(num / den);
+  }
+}
+
 // -------------------------------------------------------------- host side
 
 bool mfma_path(kl_dtype dtype, int head_dim, int page_size) {
@@ -1082,8 +1184,10 @@ constexpr int kBalancedWgPerCu = KL_DECODE_BALANCED_WG_PER_CU;
 constexpr size_t kAlign = 256;
 size_t align_up(size_t n) { return (n + kAlign - 1) / kAlign * kAlign; }
 
+// partials: a pass of cascade decode, which always takes uniform splits and
+// writes fp32 partials (workspace sized for them even with one split).
 int make_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads, int head_dim, int page_size,
-              int max_pages, int num_splits, int cu_count, Plan* p) {
+              int max_pages, int num_splits, int cu_count, Plan* p, bool partials = false) {
   if (batch < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 || max_pages < 0) {
     return fail(KL_ERR_INVALID_ARGUMENT, "batch, heads, head_dim, page_size and max_pages must be positive");
   }
@@ -1106,8 +1210,8 @@ int make_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads, int 
   const int cus = cu_count > 0 ? cu_count : 256;
   const int64_t units = std::max<int64_t>(1, static_cast<int64_t>(batch) * num_kv_heads * p->head_groups);
   const bool mfma = mfma_path(dtype, head_dim, page_size);
-  if (num_splits == KL_SPLITS_BALANCED && !mfma) num_splits = 0;  // the VALU path has uniform splits only
-  if (mfma && (num_splits == KL_SPLITS_BALANCED || (num_splits == 0 && (units < cus || KL_DECODE_BALANCE_ALWAYS)))) {
+  if (num_splits == KL_SPLITS_BALANCED && (!mfma || partials)) num_splits = 0;  // uniform splits only
+  if (mfma && !partials && (num_splits == KL_SPLITS_BALANCED || (num_splits == 0 && (units < cus || KL_DECODE_BALANCE_ALWAYS)))) {
     // Requested, or fewer units than CUs: pages balanced across sequences on the device.
     const int64_t upper = units * pages;  // list length if every sequence were full
     const int64_t grid = std::max<int64_t>(
@@ -1138,7 +1242,7 @@ int make_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads, int 
   s = static_cast<int>(cdiv(pages, pps));
   p->num_splits = s;
   p->pages_per_split = pps;
-  if (s > 1) {
+  if (s > 1 || partials) {
     const size_t rows = static_cast<size_t>(batch) * num_q_heads * s;
     p->o_bytes = align_up(rows * head_dim * sizeof(float));
     p->ws_bytes = p->o_bytes + align_up(rows * sizeof(float));
@@ -1360,6 +1464,9 @@ int decode_entry(kl_dtype dtype, bool kv8, void* out, const void* q, const void*
   a.grid = p.grid;
   a.heads_per_wg = p.heads_per_wg;
   a.scale_log2 = scale * kLog2e;
+  a.q_fold = a.group;
+  a.q_heads = num_q_heads;
+  a.force_partial = 0;
 
   const bool mfma = mfma_path(dtype, head_dim, page_size);
   switch (dtype) {
@@ -1398,4 +1505,189 @@ extern "C" int kl_paged_decode_attention_fp8(kl_dtype dtype, void* out, const vo
   return kl::decode_entry(dtype, true, out, q, k_cache, v_cache, k_scale, v_scale, block_table, seq_lens, batch,
                           num_q_heads, num_kv_heads, head_dim, page_size, block_table_stride, max_pages, scale,
                           num_splits, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+}
+
+// ------------------------------------------------------- cascade entry points
+
+namespace kl {
+namespace {
+
+struct CascadePlan {
+  Plan pre;        // shared-prefix pass (batch 1, folded group)
+  Plan suf;        // per-sequence pass
+  size_t pre_bytes;
+  size_t ws_bytes;
+};
+
+int cascade_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads, int head_dim, int page_size,
+                 int prefix_pages, int max_pages, int cu_count, CascadePlan* cp) {
+  if (dtype != KL_DTYPE_F16 && dtype != KL_DTYPE_BF16) {
+    return fail(KL_ERR_UNSUPPORTED, "cascade decode needs fp16 or bf16");
+  }
+  if (!mfma_path(dtype, head_dim, page_size)) {
+    return fail(KL_ERR_UNSUPPORTED, "cascade decode needs head_dim 32, 64, 128 or 256 and page_size a multiple of 16");
+  }
+  if (batch < 0 || num_kv_heads <= 0 || num_q_heads <= 0 || prefix_pages < 0 || max_pages < 0) {
+    return fail(KL_ERR_INVALID_ARGUMENT, "batch, heads and page counts must be non-negative");
+  }
+  if (num_q_heads % num_kv_heads != 0) {
+    return fail(KL_ERR_INVALID_ARGUMENT, "num_q_heads must be a multiple of num_kv_heads");
+  }
+  const int64_t folded = static_cast<int64_t>(std::max(batch, 1)) * (num_q_heads / num_kv_heads);
+  if (folded * num_kv_heads > 0x7fffffffLL) return fail(KL_ERR_UNSUPPORTED, "batch * num_q_heads too large");
+  int st = make_plan(dtype, 1, static_cast<int>(folded * num_kv_heads), num_kv_heads, head_dim, page_size,
+                     std::max(prefix_pages, 1), 0, cu_count, &cp->pre, true);
+  if (st != KL_OK) return st;
+  st = make_plan(dtype, std::max(batch, 1), num_q_heads, num_kv_heads, head_dim, page_size, std::max(max_pages, 1),
+                 0, cu_count, &cp->suf, true);
+  if (st != KL_OK) return st;
+  cp->pre_bytes = align_up(cp->pre.ws_bytes);
+  cp->ws_bytes = cp->pre_bytes + cp->suf.ws_bytes;
+  return ok();
+}
+
+template <typename E>
+int cascade_launch(const DecodeArgs& base, const CascadePlan& cp, const int32_t* prefix_block_table,
+                   const int32_t* prefix_len, int prefix_pages, const int32_t* block_table, const int32_t* seq_lens,
+                   int64_t bt_stride, int max_pages, char* ws, int head_dim, hipStream_t stream) {
+  const int batch = base.batch;
+  const int num_q_heads = base.num_q_heads;
+  const int group = base.group;
+  if (prefix_pages > 0) {
+    DecodeArgs a = base;
+    a.block_table = prefix_block_table;
+    a.seq_lens = prefix_len;
+    a.bt_stride = prefix_pages;
+    a.batch = 1;
+    a.group = batch * group;
+    a.num_q_heads = a.num_kv_heads * a.group;
+    a.max_pages = prefix_pages;
+    a.num_splits = cp.pre.num_splits;
+    a.pages_per_split = cp.pre.pages_per_split;
+    a.head_groups = cp.pre.head_groups;
+    a.heads_per_wg = cp.pre.heads_per_wg;
+    a.o_part = reinterpret_cast<float*>(ws);
+    a.lse_part = reinterpret_cast<float*>(ws + cp.pre.o_bytes);
+    const int64_t wgs = static_cast<int64_t>(a.num_kv_heads) * a.head_groups * a.num_splits;
+    if (wgs > 0x7fffffffLL) return fail(KL_ERR_UNSUPPORTED, "too many workgroups");
+    int st = launch_uniform_mfma<E, E>(a, head_dim, static_cast<unsigned>(wgs), stream);
+    if (st != KL_OK) return st;
+    st = check_launch("cascade prefix pass launch");
+    if (st != KL_OK) return st;
+  }
+  DecodeArgs a = base;
+  a.block_table = block_table;
+  a.seq_lens = seq_lens;
+  a.bt_stride = bt_stride;
+  a.max_pages = max_pages;
+  a.num_splits = cp.suf.num_splits;
+  a.pages_per_split = cp.suf.pages_per_split;
+  a.head_groups = cp.suf.head_groups;
+  a.heads_per_wg = cp.suf.heads_per_wg;
+  a.o_part = reinterpret_cast<float*>(ws + cp.pre_bytes);
+  a.lse_part = reinterpret_cast<float*>(ws + cp.pre_bytes + cp.suf.o_bytes);
+  const int64_t wgs = static_cast<int64_t>(batch) * a.num_kv_heads * a.head_groups * a.num_splits;
+  if (wgs > 0x7fffffffLL) return fail(KL_ERR_UNSUPPORTED, "too many workgroups");
+  int st = launch_uniform_mfma<E, E>(a, head_dim, static_cast<unsigned>(wgs), stream);
+  if (st != KL_OK) return st;
+  st = check_launch("cascade suffix pass launch");
+  if (st != KL_OK) return st;
+
+  CascadeArgs c;
+  c.p_o = reinterpret_cast<const float*>(ws);
+  c.p_lse = reinterpret_cast<const float*>(ws + cp.pre.o_bytes);
+  c.prefix_len = prefix_len;
+  c.prefix_pages = prefix_pages;
+  c.p_splits = cp.pre.num_splits;
+  c.p_pps = cp.pre.pages_per_split;
+  c.s_o = a.o_part;
+  c.s_lse = a.lse_part;
+  c.seq_lens = seq_lens;
+  c.max_pages = max_pages;
+  c.s_splits = cp.suf.num_splits;
+  c.s_pps = cp.suf.pages_per_split;
+  c.out = base.out;
+  c.batch = batch;
+  c.num_q_heads = num_q_heads;
+  c.group = group;
+  c.page_size = base.page_size;
+  cascade_merge_kernel<E><<<static_cast<unsigned>(static_cast<int64_t>(batch) * num_q_heads), 64, 0, stream>>>(
+      c, head_dim);
+  return check_launch("cascade merge kernel launch");
+}
+
+}  // namespace
+}  // namespace kl
+
+extern "C" int kl_cascade_decode_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                      int page_size, int prefix_pages, int max_pages, int cu_count,
+                                      size_t* out_workspace) {
+  using namespace kl;
+  if (cu_count <= 0) cu_count = current_cu_count();
+  CascadePlan cp;
+  const int st = cascade_plan(dtype, batch, num_q_heads, num_kv_heads, head_dim, page_size, prefix_pages, max_pages,
+                              cu_count, &cp);
+  if (st != KL_OK) return st;
+  if (out_workspace) *out_workspace = cp.ws_bytes;
+  return ok();
+}
+
+extern "C" int kl_cascade_decode_attention(kl_dtype dtype, void* out, const void* q, const void* k_cache,
+                                           const void* v_cache, const int32_t* prefix_block_table,
+                                           const int32_t* prefix_len, int prefix_pages,
+                                           const int32_t* block_table, const int32_t* seq_lens, int batch,
+                                           int num_q_heads, int num_kv_heads, int head_dim, int page_size,
+                                           int64_t block_table_stride, int max_pages, float scale, void* workspace,
+                                           size_t workspace_bytes, kl_stream_t stream) {
+  using namespace kl;
+  if (batch == 0) return ok();
+  CascadePlan cp;
+  int st = cascade_plan(dtype, batch, num_q_heads, num_kv_heads, head_dim, page_size, prefix_pages, max_pages,
+                        current_cu_count(), &cp);
+  if (st != KL_OK) return st;
+  if (!out || !q || !k_cache || !v_cache || !block_table || !seq_lens || !prefix_len ||
+      (prefix_pages > 0 && !prefix_block_table)) {
+    return fail(KL_ERR_INVALID_ARGUMENT, "tensor pointers must be non-null");
+  }
+  if (max_pages < 1) return fail(KL_ERR_INVALID_ARGUMENT, "max_pages must be >= 1");
+  if (block_table_stride < max_pages && batch > 1) {
+    return fail(KL_ERR_INVALID_ARGUMENT, "block_table_stride must be >= max_pages");
+  }
+  const uintptr_t align_mask = 15;
+  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache) |
+       reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(workspace)) & align_mask) {
+    return fail(KL_ERR_INVALID_ARGUMENT, "q, out, the caches and the workspace must be 16-byte aligned");
+  }
+  if (workspace == nullptr || workspace_bytes < cp.ws_bytes) {
+    return fail(KL_ERR_WORKSPACE, "workspace smaller than kl_cascade_decode_plan reported");
+  }
+  const int64_t token_stride = static_cast<int64_t>(num_kv_heads) * head_dim;
+  if (token_stride > 0x7fffffffLL / 64) return fail(KL_ERR_UNSUPPORTED, "num_kv_heads * head_dim too large");
+
+  DecodeArgs a{};
+  a.q = q;
+  a.k = k_cache;
+  a.v = v_cache;
+  a.out = out;
+  a.k_scale = nullptr;
+  a.v_scale = nullptr;
+  a.page_stride = static_cast<int64_t>(page_size) * num_kv_heads * head_dim;
+  a.token_stride = static_cast<int>(token_stride);
+  a.batch = batch;
+  a.num_q_heads = num_q_heads;
+  a.num_kv_heads = num_kv_heads;
+  a.group = num_q_heads / num_kv_heads;
+  a.page_size = page_size;
+  a.grid = 0;
+  a.scale_log2 = scale * kLog2e;
+  a.q_fold = a.group;
+  a.q_heads = num_q_heads;
+  a.force_partial = 1;
+  const auto s = reinterpret_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  return dtype == KL_DTYPE_F16
+             ? cascade_launch<F16>(a, cp, prefix_block_table, prefix_len, prefix_pages, block_table, seq_lens,
+                                   block_table_stride, max_pages, ws, head_dim, s)
+             : cascade_launch<BF16>(a, cp, prefix_block_table, prefix_len, prefix_pages, block_table, seq_lens,
+                                    block_table_stride, max_pages, ws, head_dim, s);
 }

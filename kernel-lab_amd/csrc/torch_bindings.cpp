@@ -16,7 +16,12 @@
 //                              Tensor block_table, Tensor seq_lens, float scale,
 //                              Tensor k_scale, Tensor v_scale, int num_splits, int max_seq_len) -> ()
 // for a float8_e4m3fn cache with fp32 per-KV-head scales (the FP8 KV cache the
-// reference lists as planned work, README.md:98).
+// reference lists as planned work, README.md:98), and
+//   cascade_decode_attention(Tensor! out, Tensor q, Tensor k_cache, Tensor v_cache,
+//                            Tensor prefix_block_table, Tensor prefix_len,
+//                            Tensor block_table, Tensor seq_lens, float scale) -> ()
+// for a prefix shared by every sequence (docs/design.md:96-100 of the reference
+// names cascade/shared-prefix attention).
 //
 // Outputs are caller-allocated ("Tensor!" = mutated in place). The only
 // allocation here is the split-KV workspace, taken from PyTorch's caching
@@ -212,6 +217,64 @@ void paged_decode_attention_fp8(at::Tensor& out, const at::Tensor& q, const at::
                     &v_scale);
 }
 
+// Shared-prefix decode: attention over prefix tokens, then each sequence's own.
+void cascade_decode_attention(at::Tensor& out, const at::Tensor& q, const at::Tensor& k_cache,
+                              const at::Tensor& v_cache, const at::Tensor& prefix_block_table,
+                              const at::Tensor& prefix_len, const at::Tensor& block_table,
+                              const at::Tensor& seq_lens, double scale) {
+  const auto dev = q.device();
+  const std::initializer_list<const at::Tensor*> all = {&k_cache, &v_cache,    &out,    &prefix_block_table,
+                                                        &prefix_len, &block_table, &seq_lens};
+  for (const at::Tensor* t : all) {
+    TORCH_CHECK(t->is_cuda() && t->device() == dev, "tensors must share q's GPU");
+  }
+  TORCH_CHECK(q.dim() == 3 && k_cache.dim() == 4, "q is [batch, heads, dim]; caches are 4-D");
+  TORCH_CHECK(q.is_contiguous() && out.is_contiguous() && k_cache.is_contiguous() && v_cache.is_contiguous(),
+              "q, out and both caches must be contiguous");
+  TORCH_CHECK(k_cache.sizes() == v_cache.sizes() && out.sizes() == q.sizes(), "cache or output shapes differ");
+  TORCH_CHECK(q.scalar_type() == k_cache.scalar_type() && q.scalar_type() == v_cache.scalar_type() &&
+                  q.scalar_type() == out.scalar_type(),
+              "q, caches and out must share a dtype");
+  TORCH_CHECK(prefix_block_table.scalar_type() == at::kInt && prefix_block_table.dim() == 1 &&
+                  prefix_block_table.is_contiguous(),
+              "prefix_block_table is a contiguous 1-D int32 tensor");
+  TORCH_CHECK(prefix_len.scalar_type() == at::kInt && prefix_len.numel() == 1, "prefix_len is one int32");
+  TORCH_CHECK(block_table.scalar_type() == at::kInt && seq_lens.scalar_type() == at::kInt &&
+                  block_table.dim() == 2 && seq_lens.dim() == 1 && block_table.stride(-1) == 1 &&
+                  seq_lens.is_contiguous(),
+              "block_table is 2-D int32 with contiguous rows; seq_lens contiguous 1-D int32");
+  const int batch = static_cast<int>(q.size(0));
+  const int num_q_heads = static_cast<int>(q.size(1));
+  const int head_dim = static_cast<int>(q.size(2));
+  const int page_size = static_cast<int>(k_cache.size(1));
+  const int num_kv_heads = static_cast<int>(k_cache.size(2));
+  TORCH_CHECK(k_cache.size(3) == head_dim, "cache head_dim differs from q");
+  TORCH_CHECK(num_kv_heads > 0 && num_q_heads % num_kv_heads == 0, "num_q_heads must be a multiple of num_kv_heads");
+  TORCH_CHECK(block_table.size(0) == batch && seq_lens.size(0) == batch,
+              "block_table and seq_lens need one row per sequence");
+  if (batch == 0) return;
+  const int64_t max_pages = block_table.size(1);
+  TORCH_CHECK(max_pages >= 1, "block_table needs at least one column");
+  const int64_t bt_stride = batch > 1 ? block_table.stride(0) : block_table.size(1);
+  const int prefix_pages = static_cast<int>(prefix_block_table.numel());
+
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(dev);
+  const kl_dtype dtype = to_kl_dtype(q.scalar_type());
+  size_t ws_bytes = 0;
+  check_status(kl_cascade_decode_plan(dtype, batch, num_q_heads, num_kv_heads, head_dim, page_size, prefix_pages,
+                                      static_cast<int>(max_pages), 0, &ws_bytes),
+               "cascade_decode_attention planning");
+  at::Tensor workspace = at::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
+  check_status(kl_cascade_decode_attention(
+                   dtype, out.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                   prefix_pages > 0 ? prefix_block_table.data_ptr<int32_t>() : nullptr,
+                   prefix_len.data_ptr<int32_t>(), prefix_pages, block_table.data_ptr<int32_t>(),
+                   seq_lens.data_ptr<int32_t>(), batch, num_q_heads, num_kv_heads, head_dim, page_size, bt_stride,
+                   static_cast<int>(max_pages), static_cast<float>(scale), workspace.data_ptr(), ws_bytes,
+                   current_stream(dev)),
+               "cascade_decode_attention");
+}
+
 }  // namespace
 
 TORCH_LIBRARY(kernel_lab, m) {
@@ -228,6 +291,9 @@ TORCH_LIBRARY(kernel_lab, m) {
       "paged_decode_attention_fp8(Tensor! out, Tensor q, Tensor k_cache, Tensor v_cache, "
       "Tensor block_table, Tensor seq_lens, float scale, Tensor k_scale, Tensor v_scale, "
       "int num_splits=0, int max_seq_len=0) -> ()");
+  m.def(
+      "cascade_decode_attention(Tensor! out, Tensor q, Tensor k_cache, Tensor v_cache, "
+      "Tensor prefix_block_table, Tensor prefix_len, Tensor block_table, Tensor seq_lens, float scale) -> ()");
 }
 
 // ROCm tensors carry PyTorch's CUDA dispatch key.
@@ -238,4 +304,5 @@ TORCH_LIBRARY_IMPL(kernel_lab, CUDA, m) {
   m.impl("paged_decode_attention", &paged_decode_attention);
   m.impl("paged_decode_attention.splits", &paged_decode_attention_splits);
   m.impl("paged_decode_attention_fp8", &paged_decode_attention_fp8);
+  m.impl("cascade_decode_attention", &cascade_decode_attention);
 }

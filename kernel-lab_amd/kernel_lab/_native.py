@@ -38,6 +38,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _i32,
         [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i64, _i32, _f32, _i32, _vp, _sz, _vp],
     ),
+    "kl_cascade_decode_plan": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_sz)]),
+    "kl_cascade_decode_attention": (
+        _i32,
+        [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i64, _i32, _f32, _vp, _sz, _vp],
+    ),
     "kl_paged_decode_attention_fp8": (
         _i32,
         [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i64, _i32, _f32, _i32, _vp, _sz, _vp],

@@ -13,6 +13,8 @@ the measured configurations):
   (64/8/128, batch 8, contexts 32768 and 131072);
 * decode-fp8: the FP8 (E4M3) cache against a 16-bit cache holding the same
   values, at the headline, ragged and long-context shapes;
+* cascade: shared-prefix decode against plain paged decode over the same
+  pages (prefixes of 4096-32768 tokens shared by 16-64 sequences);
 * copy: a 1 GiB device copy (the streaming ceiling, and the counter
   calibration kernel for the profiles).
 
@@ -37,7 +39,7 @@ import torch
 
 from kernel_lab import ops
 from kernel_lab.bench.roofline import GPUPeak, Work, decode_attention_work, lookup, rms_norm_work
-from kernel_lab.kv_cache import device_decode_problem, quantize_fp8
+from kernel_lab.kv_cache import device_decode_problem, quantize_fp8, random_cascade_problem
 
 DTYPES = {"float16": torch.float16, "bfloat16": torch.bfloat16, "float32": torch.float32}
 
@@ -301,6 +303,52 @@ def decode_fp8_suite(peak: GPUPeak | None, timer, shape: str | None = None) -> l
     return rows
 
 
+# ------------------------------------------------------------------ cascade
+
+
+def cascade_cases() -> list[tuple[str, int, list[int], int, int, torch.dtype]]:
+    return [
+        ("32/8/128 b64 prefix 4096 + 512 own", 4096, [512] * 64, 32, 8, torch.float16),
+        ("32/8/128 b32 prefix 16384 + 256 own", 16384, [256] * 32, 32, 8, torch.float16),
+        ("64/8/128 b16 prefix 32768 + 1024 own", 32768, [1024] * 16, 64, 8, torch.bfloat16),
+    ]
+
+
+def cascade_suite(peak: GPUPeak | None, timer, shape: str | None = None) -> list[Row]:
+    """Shared-prefix decode against plain paged decode over the same pages
+    (each sequence's table = prefix pages + own pages). GB/s counts the bytes
+    each must read: the prefix once for cascade, once per sequence for plain."""
+    rows: list[Row] = []
+    d, page = 128, 16
+    for label, plen, lens, hq, hkv, dt in cascade_cases():
+        if shape and shape not in label:
+            continue
+        q, c = random_cascade_problem(plen, lens, hq, hkv, d, page, dtype=dt, device="cuda")
+        flat = c.flattened()
+        scale = d**-0.5
+        o_plain, o_casc = torch.empty_like(q), torch.empty_like(q)
+        impls: dict[str, Callable[[], torch.Tensor]] = {
+            "hip paged decode (planner)": lambda: ops.paged_decode_attention(
+                q, flat.k_cache, flat.v_cache, flat.block_table, flat.seq_lens, scale, out=o_plain
+            ),
+            "hip cascade": lambda: ops.cascade_decode_attention(
+                q, c.kv.k_cache, c.kv.v_cache, c.prefix_block_table, c.prefix_len, c.kv.block_table,
+                c.kv.seq_lens, scale, out=o_casc
+            ),
+        }
+        elem = 2
+        plain = decode_attention_work([plen + n for n in lens], hq, hkv, d, elem)
+        prefix_once = decode_attention_work([plen + sum(lens)], hq, hkv, d, elem)
+        # q and out are counted for every sequence, the prefix's K/V once.
+        q_out = 2 * len(lens) * hq * d * elem
+        casc = Work(bytes=prefix_once.bytes - 2 * hq * d * elem + q_out, flops=plain.flops)
+        work = {"hip paged decode (planner)": plain, "hip cascade": casc}
+        rows += measure("cascade_decode", label, impls, work, peak, "hip paged decode (planner)", 3e-2, timer)
+        del q, c, flat, o_plain, o_casc, impls
+        torch.cuda.empty_cache()
+    return rows
+
+
 # ------------------------------------------------------------------- copy
 
 
@@ -343,7 +391,7 @@ def main(argv: list[str] | None = None) -> int:
     parser = argparse.ArgumentParser(
         prog="python -m kernel_lab.bench", description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter
     )
-    parser.add_argument("suite", choices=["rmsnorm", "decode", "decode-fp8", "copy", "all"])
+    parser.add_argument("suite", choices=["rmsnorm", "decode", "decode-fp8", "cascade", "copy", "all"])
     parser.add_argument("--dtype", choices=list(DTYPES), default="float16")
     parser.add_argument("--peak-gbps", type=float, help="override the spec-sheet DRAM bandwidth")
     parser.add_argument("--compile", action="store_true", help="add the torch.compile RMSNorm baseline")
@@ -379,6 +427,8 @@ def main(argv: list[str] | None = None) -> int:
         rows += decode_suite(dtype, peak, timer, args.splits, args.baseline_max_gb * 1e9, args.shape)
     if args.suite in ("decode-fp8", "all"):
         rows += decode_fp8_suite(peak, timer, args.shape)
+    if args.suite in ("cascade", "all"):
+        rows += cascade_suite(peak, timer, args.shape)
     if args.suite == "copy":
         rows += copy_suite(peak, timer)
 

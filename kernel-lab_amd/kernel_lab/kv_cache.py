@@ -227,3 +227,70 @@ def quantize_fp8(kv: PagedKV) -> tuple[PagedKV, torch.Tensor, torch.Tensor]:
         scales.append(scale)
     q8 = PagedKV(out[0], out[1], kv.block_table, kv.seq_lens, kv.page_size)
     return q8, scales[0], scales[1]
+
+
+@dataclass
+class CascadeKV:
+    """A paged pool holding a shared prefix and each sequence's own tokens."""
+
+    kv: PagedKV  # block_table / seq_lens: each sequence's own tokens (may be 0)
+    prefix_block_table: torch.Tensor  # [cdiv(prefix_len, page_size)] int32
+    prefix_len: int
+
+    def flattened(self) -> PagedKV:
+        """The same attention as plain paged decode: each sequence's table is
+        the prefix pages followed by its own (needs a page-aligned prefix)."""
+        page = self.kv.page_size
+        if self.prefix_len % page:
+            raise ValueError("flattening needs prefix_len to be a multiple of page_size")
+        own_pages = [pages_for(int(n), page) for n in self.kv.seq_lens.tolist()]
+        npre = self.prefix_block_table.numel()
+        table = torch.zeros(
+            (len(own_pages), npre + max(own_pages + [0])), dtype=torch.int32, device=self.kv.block_table.device
+        )
+        table[:, :npre] = self.prefix_block_table
+        for b, n in enumerate(own_pages):
+            table[b, npre : npre + n] = self.kv.block_table[b, :n]
+        return PagedKV(self.kv.k_cache, self.kv.v_cache, table, self.kv.seq_lens + self.prefix_len, page)
+
+
+def random_cascade_problem(
+    prefix_len: int,
+    seq_lens: list[int],
+    num_q_heads: int,
+    num_kv_heads: int,
+    head_dim: int,
+    page_size: int,
+    dtype: torch.dtype = torch.float16,
+    device: str | torch.device = "cpu",
+    seed: int = 0,
+    poison: float = float("nan"),
+) -> tuple[torch.Tensor, CascadeKV]:
+    """Random queries, a shared prefix of ``prefix_len`` tokens and per-sequence
+    suffixes of ``seq_lens`` tokens (0 allowed), paged into one pool with the
+    rules of build_paged_kv (the prefix is paged first, as one more sequence).
+    Spare pages and the tails of last pages hold ``poison``.
+    """
+    generator = torch.Generator().manual_seed(seed)
+
+    def rand(*shape: int) -> torch.Tensor:
+        return torch.randn(*shape, generator=generator).to(dtype=dtype)
+
+    q = rand(len(seq_lens), num_q_heads, head_dim)
+    # Every paged "sequence" needs a token; a zero-length prefix or suffix gets
+    # one unreferenced token and a length of 0.
+    lens = [max(prefix_len, 1)] + [max(n, 1) for n in seq_lens]
+    keys = [rand(n, num_kv_heads, head_dim) for n in lens]
+    values = [rand(n, num_kv_heads, head_dim) for n in lens]
+    # Tails of last pages hold the poison too: only masking keeps them out.
+    pool = build_paged_kv(keys, values, page_size, seed=seed, poison=poison, tail=poison)
+    npre = pages_for(prefix_len, page_size)
+    prefix_table = pool.block_table[0, :npre].clone()
+    own = PagedKV(
+        k_cache=pool.k_cache.to(device),
+        v_cache=pool.v_cache.to(device),
+        block_table=pool.block_table[1:].contiguous().to(device),
+        seq_lens=torch.tensor(seq_lens, dtype=torch.int32, device=device),
+        page_size=page_size,
+    )
+    return q.to(device), CascadeKV(own, prefix_table.to(device), prefix_len)

@@ -165,6 +165,41 @@ def paged_decode_attention(
     return out
 
 
+def cascade_decode_attention(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    prefix_block_table: torch.Tensor,
+    prefix_len: int | torch.Tensor,
+    block_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    scale: float | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Decode with a prefix shared by every sequence (cascade attention).
+
+    Sequence b attends over the ``prefix_len`` tokens on pages
+    ``prefix_block_table`` (1-D int32, shared) followed by its own
+    ``seq_lens[b]`` tokens on ``block_table[b]``; both sets of pages live in
+    ``k_cache`` / ``v_cache``. ``prefix_len`` may be a one-element int32 device
+    tensor (no host sync) or an int. The prefix's K/V is streamed once per 32
+    query heads of the whole batch instead of once per sequence.
+    """
+    _check_decode(q, k_cache, v_cache)
+    _native.require_ops()
+    scale = q.shape[-1] ** -0.5 if scale is None else float(scale)
+    q = q.contiguous()
+    if out is None:
+        out = torch.empty_like(q)
+    if not isinstance(prefix_len, torch.Tensor):
+        prefix_len = torch.tensor([int(prefix_len)], dtype=torch.int32, device=q.device)
+    prefix_block_table = prefix_block_table.reshape(-1).to(torch.int32).contiguous()
+    torch.ops.kernel_lab.cascade_decode_attention(
+        out, q, k_cache, v_cache, prefix_block_table, prefix_len.reshape(1), block_table, seq_lens, scale
+    )
+    return out
+
+
 def _head_scales(s: torch.Tensor | float, num_kv_heads: int, device: torch.device) -> torch.Tensor:
     """Per-KV-head float32 scales on the device: a tensor of num_kv_heads
     values, or one number (or one-element tensor) for every head."""

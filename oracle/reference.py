@@ -89,6 +89,46 @@ def paged_decode_attention_fp8(
     return paged_decode_attention(q.cpu(), k, v, block_table, seq_lens, scale)
 
 
+def cascade_decode_attention(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    prefix_block_table: torch.Tensor,
+    prefix_len: int,
+    block_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    scale: float | None = None,
+) -> torch.Tensor:
+    """Shared-prefix decode: sequence b attends over the prefix's first
+    prefix_len tokens (pages prefix_block_table) followed by its own seq_lens[b]
+    tokens, with paged_decode_attention's float32 math over the concatenation.
+
+    The original project names this FlashInfer feature (docs/design.md:96-100)
+    without implementing it; its definition is attention over the concatenated
+    token sequence.
+    """
+    batch, num_q_heads, head_dim = q.shape
+    num_kv_heads = k_cache.shape[2]
+    group = num_q_heads // num_kv_heads
+    scale = head_dim**-0.5 if scale is None else scale
+    ptable = prefix_block_table.cpu().reshape(-1)
+    pk = _gather(k_cache, ptable, prefix_len)
+    pv = _gather(v_cache, ptable, prefix_len)
+    lens = [int(n) for n in seq_lens.tolist()]
+    table = block_table.cpu()
+    out = torch.empty_like(q)
+    for b in range(batch):
+        k = torch.cat([pk, _gather(k_cache, table[b], lens[b])])
+        v = torch.cat([pv, _gather(v_cache, table[b], lens[b])])
+        if k.shape[0] == 0:
+            out[b] = 0
+            continue
+        qb = q[b].float().reshape(num_kv_heads, group, head_dim)
+        probs = torch.softmax(torch.einsum("hgd,lhd->hgl", qb, k) * scale, dim=-1)
+        out[b] = torch.einsum("hgl,lhd->hgd", probs, v).reshape(num_q_heads, head_dim).to(q.dtype)
+    return out
+
+
 def dense_decode_attention(
     q: torch.Tensor, keys: list[torch.Tensor], values: list[torch.Tensor], scale: float | None = None
 ) -> torch.Tensor:
