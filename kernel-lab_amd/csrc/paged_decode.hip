@@ -206,13 +206,12 @@ struct MfmaLds {
 
 // Register pipeline depth: blocks whose K and V are held in VGPRs at once
 // (one being processed, the rest in flight); 8 KiB per block at D = 128 with
-// a 16-bit cache. Measured on MI355X at D = 128: 2 stages beat 3..6 (more
-// bytes in flight per wave past ~16 KiB lowers HBM throughput for this access
-// pattern). An FP8 cache holds half the bytes per block.
+// a 16-bit cache, 4 KiB with FP8. Measured on MI355X at D = 128: 2 stages
+// beat 3..6 for both cache formats (FP8 B=64 ctx 4096: 103 us at 2 stages,
+// 107-110 us at 3-6).
 template <int D, int NT, int KB>
 constexpr int mfma_stages() {
   if (KL_DECODE_STAGES > 0) return KL_DECODE_STAGES;
-  if (KB == 1) return D <= 64 ? 8 : D == 128 ? (NT == 2 ? 3 : 4) : 2;
   return D <= 64 ? 6 : 2;
 }
 
