@@ -44,6 +44,7 @@
 // token; each lane keeps an online softmax per query head and lanes merge by
 // the log-sum-exp rule at the end.
 #include <algorithm>
+#include <cstdlib>
 #include <cmath>
 #include <type_traits>
 
@@ -1132,9 +1133,18 @@ __global__ void __launch_bounds__(64) cascade_merge_kernel(const CascadeArgs c, 
 
 // -------------------------------------------------------------- host side
 
+// Shapes the MFMA kernels serve.
 bool mfma_path(kl_dtype dtype, int head_dim, int page_size) {
   return (dtype == KL_DTYPE_F16 || dtype == KL_DTYPE_BF16) && page_size % kBlock == 0 &&
          (head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256);
+}
+
+// KL_DECODE_FORCE_VALU=1 in the environment (read on every call) sends 16-bit
+// decode to the VALU kernel, so benchmarks can time the two paths on the same
+// shapes; the FP8 and cascade entry points ignore it.
+bool valu_forced() {
+  const char* v = std::getenv("KL_DECODE_FORCE_VALU");
+  return v != nullptr && v[0] == '1';
 }
 
 bool valu_head_dim_ok(kl_dtype dtype, int head_dim) {
@@ -1153,15 +1163,15 @@ bool valu_head_dim_ok(kl_dtype dtype, int head_dim) {
 
 // Query heads one workgroup takes from a GQA group, and the resulting number of
 // workgroups per (sequence, KV head, split).
-void head_tiling(kl_dtype dtype, int head_dim, int page_size, int group, int* per_wg, int* groups) {
+void head_tiling(bool mfma, int head_dim, int group, int* per_wg, int* groups) {
   int cap;
-  if (mfma_path(dtype, head_dim, page_size)) {
+  if (mfma) {
     cap = (group > 16 && head_dim <= 128) ? 32 : 16;
   } else {
     cap = 8;
   }
   int per = std::min(group, cap);
-  if (!mfma_path(dtype, head_dim, page_size)) {
+  if (!mfma) {
     per = per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : 8;  // template sizes of the VALU kernel
   }
   *per_wg = per;
@@ -1185,8 +1195,9 @@ size_t align_up(size_t n) { return (n + kAlign - 1) / kAlign * kAlign; }
 
 // partials: a pass of cascade decode, which always takes uniform splits and
 // writes fp32 partials (workspace sized for them even with one split).
+// use_mfma false: plan for the VALU kernel even where the MFMA one could run.
 int make_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads, int head_dim, int page_size,
-              int max_pages, int num_splits, int cu_count, Plan* p, bool partials = false) {
+              int max_pages, int num_splits, int cu_count, Plan* p, bool partials = false, bool use_mfma = true) {
   if (batch < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 || max_pages < 0) {
     return fail(KL_ERR_INVALID_ARGUMENT, "batch, heads, head_dim, page_size and max_pages must be positive");
   }
@@ -1199,16 +1210,16 @@ int make_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads, int 
   if (dtype != KL_DTYPE_F32 && dtype != KL_DTYPE_F16 && dtype != KL_DTYPE_BF16) {
     return fail(KL_ERR_UNSUPPORTED, "dtype must be f32, f16 or bf16");
   }
-  if (!mfma_path(dtype, head_dim, page_size) && !valu_head_dim_ok(dtype, head_dim)) {
+  const bool mfma = use_mfma && mfma_path(dtype, head_dim, page_size);
+  if (!mfma && !valu_head_dim_ok(dtype, head_dim)) {
     return fail(KL_ERR_UNSUPPORTED, "head_dim must be 16, 32, 64, 128 or 256");
   }
   const int group = num_q_heads / num_kv_heads;
-  head_tiling(dtype, head_dim, page_size, group, &p->heads_per_wg, &p->head_groups);
+  head_tiling(mfma, head_dim, group, &p->heads_per_wg, &p->head_groups);
   const int pages = std::max(max_pages, 1);
   p->grid = 0;
   const int cus = cu_count > 0 ? cu_count : 256;
   const int64_t units = std::max<int64_t>(1, static_cast<int64_t>(batch) * num_kv_heads * p->head_groups);
-  const bool mfma = mfma_path(dtype, head_dim, page_size);
   if (num_splits == KL_SPLITS_BALANCED && (!mfma || partials)) num_splits = 0;  // uniform splits only
   if (mfma && !partials && (num_splits == KL_SPLITS_BALANCED || (num_splits == 0 && (units < cus || KL_DECODE_BALANCE_ALWAYS)))) {
     // Requested, or fewer units than CUs: pages balanced across sequences on the device.
@@ -1384,8 +1395,8 @@ extern "C" int kl_paged_decode_plan(kl_dtype dtype, int batch, int num_q_heads, 
   using namespace kl;
   if (cu_count <= 0) cu_count = current_cu_count();
   Plan p;
-  const int st =
-      make_plan(dtype, batch, num_q_heads, num_kv_heads, head_dim, page_size, max_pages, num_splits, cu_count, &p);
+  const int st = make_plan(dtype, batch, num_q_heads, num_kv_heads, head_dim, page_size, max_pages, num_splits,
+                           cu_count, &p, false, !valu_forced());
   if (st != KL_OK) return st;
   if (out_num_splits) *out_num_splits = p.num_splits;
   if (out_workspace) *out_workspace = p.ws_bytes;
@@ -1412,9 +1423,10 @@ int decode_entry(kl_dtype dtype, bool kv8, void* out, const void* q, const void*
     }
     if (!k_scale || !v_scale) return fail(KL_ERR_INVALID_ARGUMENT, "k_scale and v_scale must be non-null");
   }
+  const bool use_mfma = kv8 || !valu_forced();
   Plan p;
   int st = make_plan(dtype, batch, num_q_heads, num_kv_heads, head_dim, page_size, max_pages, num_splits,
-                     current_cu_count(), &p);
+                     current_cu_count(), &p, false, use_mfma);
   if (st != KL_OK) return st;
   if (!out || !q || !k_cache || !v_cache || !block_table || !seq_lens) {
     return fail(KL_ERR_INVALID_ARGUMENT, "out, q, k_cache, v_cache, block_table and seq_lens must be non-null");
@@ -1467,7 +1479,7 @@ int decode_entry(kl_dtype dtype, bool kv8, void* out, const void* q, const void*
   a.q_heads = num_q_heads;
   a.force_partial = 0;
 
-  const bool mfma = mfma_path(dtype, head_dim, page_size);
+  const bool mfma = use_mfma && mfma_path(dtype, head_dim, page_size);
   switch (dtype) {
     case KL_DTYPE_F32:
       return launch_typed<F32, F32>(a, head_dim, false, stream);

@@ -30,6 +30,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import os
 import sys
 from collections.abc import Callable
 from dataclasses import asdict, dataclass
@@ -218,6 +219,16 @@ def decode_cases(dtype: torch.dtype) -> list[tuple[str, list[int], int, int, tor
     return cases
 
 
+def _forced_valu(fn: Callable[[], torch.Tensor]) -> torch.Tensor:
+    """Runs fn with the library's 16-bit decode sent to its VALU kernel
+    (KL_DECODE_FORCE_VALU, read by the library on every call)."""
+    os.environ["KL_DECODE_FORCE_VALU"] = "1"
+    try:
+        return fn()
+    finally:
+        del os.environ["KL_DECODE_FORCE_VALU"]
+
+
 def decode_suite(
     dtype: torch.dtype,
     peak: GPUPeak | None,
@@ -237,12 +248,17 @@ def decode_suite(
         elem = torch.tensor([], dtype=dt).element_size()
         work = decode_attention_work(lens, hq, hkv, d, elem)
         out = torch.empty_like(q)
+        out2 = torch.empty_like(q)
         impls: dict[str, Callable[[], torch.Tensor]] = {}
         # The gather baseline materialises padded K/V; skip it where that would be huge.
         gather_bytes = 2 * kv.block_table.numel() * page * hkv * d * elem
         if gather_bytes <= baseline_max_bytes:
             impls["torch (gather + matmul)"] = lambda a=args, s=scale: torch_paged_decode(*a, s)
         impls["hip split-KV (planner)"] = lambda a=args, s=scale, o=out: ops.paged_decode_attention(*a, s, out=o)
+        if dt != torch.float32:
+            impls["hip VALU kernel (planner)"] = lambda a=args, s=scale, o=out2: _forced_valu(
+                lambda: ops.paged_decode_attention(*a, s, out=o)
+            )
         for n in splits:
             impls[f"hip splits={n}"] = lambda a=args, s=scale, o=out, n=n: ops.paged_decode_attention(
                 *a, s, num_splits=n, out=o
@@ -250,7 +266,7 @@ def decode_suite(
         baseline = next(iter(impls))
         atol = 2e-2 if dt != torch.float32 else 1e-3
         rows += measure("paged_decode", label, impls, work, peak, baseline, atol, timer)
-        del q, kv, args, out, impls
+        del q, kv, args, out, out2, impls
         torch.cuda.empty_cache()
     return rows
 

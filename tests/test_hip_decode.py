@@ -315,3 +315,15 @@ def test_requested_balanced_schedule_falls_back_for_fp32(gpu_ops):
 
     q, kv, _, _ = random_decode_problem([300, 20], 8, 2, 64, 16, dtype=torch.float32, device="cuda")
     check(run(gpu_ops, q, kv, num_splits=ops.BALANCED), expected(q, kv), torch.float32)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize(("hq", "hkv", "head_dim"), [(32, 8, 128), (8, 1, 64), (16, 16, 256)])
+def test_forced_valu_kernel_on_mfma_shapes(gpu_ops, monkeypatch, hq, hkv, head_dim, dtype):
+    """KL_DECODE_FORCE_VALU=1 runs the VALU kernel (the benchmarks' comparison
+    path) on shapes the MFMA kernel normally takes; both must match the oracle."""
+    q, kv, _, _ = random_decode_problem([1, 40, 300, 17], hq, hkv, head_dim, 16, dtype=dtype, device="cuda",
+                                        poison=float("nan"))
+    monkeypatch.setenv("KL_DECODE_FORCE_VALU", "1")
+    check(run(gpu_ops, q, kv), expected(q, kv), dtype)
+    check(run(gpu_ops, q, kv, num_splits=3), expected(q, kv), dtype)
