@@ -210,7 +210,7 @@ struct MfmaLds {
 // a 16-bit cache, 4 KiB with FP8. Measured on MI355X at D = 128: 2 stages
 // beat 3..6 for both cache formats (FP8 B=64 ctx 4096: 103 us at 2 stages,
 // 107-110 us at 3-6).
-template <int D, int NT, int KB>
+template <int D>
 constexpr int mfma_stages() {
   if (KL_DECODE_STAGES > 0) return KL_DECODE_STAGES;
   return D <= 64 ? 6 : 2;
@@ -270,7 +270,7 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
   static_assert(TPL <= kBlock && kBlock % TPL == 0, "a load must stay inside its 16-token block");
   constexpr int KROW = MfmaLds<D, NT>::kKRow;
   constexpr int VROW = MfmaLds<D, NT>::kVRow;
-  constexpr int NS = mfma_stages<D, NT, KB>();
+  constexpr int NS = mfma_stages<D>();
 
   const int lane = __lane_id();
   const int wave = wave_id();
