@@ -76,6 +76,12 @@ namespace {
 #ifndef KL_DECODE_MIN_PAGES
 #define KL_DECODE_MIN_PAGES 16  // fewest pages a planned split or balanced workgroup takes
 #endif
+#ifndef KL_DECODE_XCD_REMAP
+#define KL_DECODE_XCD_REMAP 0  // give each XCD a contiguous range of work units
+#endif
+#ifndef KL_DECODE_KV_POLICY
+#define KL_DECODE_KV_POLICY kCachePolicyNT  // cache-policy bits of the K/V loads
+#endif
 
 constexpr int kWaves = KL_DECODE_WAVES;  // waves per workgroup
 constexpr int kThreads = kWaves * 64;
@@ -126,9 +132,21 @@ struct Unit {
   int page_begin, page_end;
 };
 
+// Workgroups are dispatched to the 8 XCDs round-robin (workgroup i runs on
+// XCD i % 8). This bijection on [0, n) hands XCD x a contiguous range of
+// work ids instead of every 8th one.
+__device__ __forceinline__ int xcd_remap(int pid, int n) {
+  constexpr int kXcds = 8;
+  const int per = (n + kXcds - 1) / kXcds;
+  const int tall = n - (per - 1) * kXcds;  // XCDs that get `per` ids (1 .. 8)
+  const int xcd = pid % kXcds;
+  const int local = pid / kXcds;
+  return xcd < tall ? xcd * per + local : tall * per + (xcd - tall) * (per - 1) + local;
+}
+
 __device__ __forceinline__ Unit decode_unit(const DecodeArgs& a) {
   Unit u;
-  int idx = blockIdx.x;
+  int idx = KL_DECODE_XCD_REMAP ? xcd_remap(blockIdx.x, gridDim.x) : static_cast<int>(blockIdx.x);
   u.split = idx % a.num_splits;
   idx /= a.num_splits;
   u.hg = idx % a.head_groups;
@@ -357,12 +375,12 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
   auto load_k = [&](int64_t base, u32x4 (&kf)[NL]) {
     const auto kr = make_rsrc(kc + base);
 #pragma unroll
-    for (int c = 0; c < NL; ++c) kf[c] = buffer_load16<kCachePolicyNT>(kr, kv_off[c]);
+    for (int c = 0; c < NL; ++c) kf[c] = buffer_load16<KL_DECODE_KV_POLICY>(kr, kv_off[c]);
   };
   auto load_v = [&](int64_t base, u32x4 (&vf)[NL]) {
     const auto vr = make_rsrc(vc + base);
 #pragma unroll
-    for (int c = 0; c < NL; ++c) vf[c] = buffer_load16<kCachePolicyNT>(vr, kv_off[c]);
+    for (int c = 0; c < NL; ++c) vf[c] = buffer_load16<KL_DECODE_KV_POLICY>(vr, kv_off[c]);
   };
   auto load_block = [&](int64_t base, u32x4 (&kf)[NL], u32x4 (&vf)[NL]) {
     load_k(base, kf);
