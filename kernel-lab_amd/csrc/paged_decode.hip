@@ -74,7 +74,10 @@ namespace {
 #define KL_DECODE_BALANCE_ALWAYS 0  // balanced schedule also when units fill the device
 #endif
 #ifndef KL_DECODE_MIN_PAGES
-#define KL_DECODE_MIN_PAGES 16  // fewest pages a planned split or balanced workgroup takes
+#define KL_DECODE_MIN_PAGES 16  // fewest pages a planned uniform split takes
+#endif
+#ifndef KL_DECODE_BALANCED_MIN_PAGES
+#define KL_DECODE_BALANCED_MIN_PAGES 8  // fewest pages a balanced-schedule workgroup takes
 #endif
 #ifndef KL_DECODE_XCD_REMAP
 #define KL_DECODE_XCD_REMAP 0  // give each XCD a contiguous range of work units
@@ -88,6 +91,7 @@ constexpr int kThreads = kWaves * 64;
 constexpr int kBlock = 16;     // tokens per MFMA block
 constexpr int kMaxPlannedSplits = 64;
 constexpr int kMinPagesPerSplit = KL_DECODE_MIN_PAGES;
+constexpr int kMinPagesPerBalancedWg = KL_DECODE_BALANCED_MIN_PAGES;
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct DecodeArgs {
@@ -598,7 +602,7 @@ __global__ void __launch_bounds__(kThreads, (mfma_waves_per_eu<D, NT>())) decode
 //
 // Work list: every (sequence b, KV head, head group) unit is cdiv(L_b, page
 // size) pages long; units are laid end to end, b-major. Workgroup w takes
-// positions [w*per, (w+1)*per) of that list, per = max(16, cdiv(total, grid)),
+// positions [w*per, (w+1)*per) of that list, per = max(8, cdiv(total, grid)),
 // which may span the tail of one unit and the head of the next, so every
 // workgroup streams the same number of pages however uneven the lengths are.
 // Totals and prefix sums come from seq_lens on the device (no host sync).
@@ -632,7 +636,7 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
 }
 
 __device__ __forceinline__ int64_t balanced_per(const DecodeArgs& a, int64_t total) {
-  return max(static_cast<int64_t>(kMinPagesPerSplit), (total + a.grid - 1) / a.grid);
+  return max(static_cast<int64_t>(kMinPagesPerBalancedWg), (total + a.grid - 1) / a.grid);
 }
 
 // Pages in the whole work list. Wave-uniform; every wave computes it.
@@ -647,21 +651,27 @@ __device__ __forceinline__ int64_t list_total(const DecodeArgs& a, int units_per
   return total;
 }
 
-// Length of the work list and the list position where sequence b's units
-// begin (b wave-uniform).
+// Length of the work list, the list position where sequence b's units begin
+// and sequence b's page count (b wave-uniform).
 __device__ __forceinline__ void list_prefix(const DecodeArgs& a, int units_per_seq, int b, int64_t* total,
-                                            int64_t* base) {
+                                            int64_t* base, int* pages) {
   const int lane = __lane_id();
   int64_t t = 0, pre = 0;
+  int own = 0;
   for (int b0 = 0; b0 < a.batch; b0 += 64) {
     const int bb = b0 + lane;
-    const int pl = bb < a.batch ? seq_pages(a, bb) * units_per_seq : 0;
+    const int np = bb < a.batch ? seq_pages(a, bb) : 0;
+    const int pl = np * units_per_seq;
     const int incl = wave_incl_scan(pl);
-    if (b >= b0 && b < b0 + 64) pre = t + __builtin_amdgcn_readlane(incl - pl, b - b0);
+    if (b >= b0 && b < b0 + 64) {
+      pre = t + __builtin_amdgcn_readlane(incl - pl, b - b0);
+      own = __builtin_amdgcn_readlane(np, b - b0);
+    }
     t += __builtin_amdgcn_readlane(incl, 63);
   }
   *total = t;
   *base = pre;
+  *pages = own;
 }
 
 // Where workgroup `wg` starts: its first list position `pos` (wg * per), the
@@ -955,11 +965,18 @@ __global__ void __launch_bounds__(kThreads) decode_valu_kernel(const DecodeArgs 
 
 // --------------------------------------------------------------- split merge
 
-// Merge of n partials (o_w, lse_w), w = 0 .. n-1, into one output head:
-// out[d] = sum_w 2^(lse_w - M) o_w[d] / sum_w 2^(lse_w - M), M = max_w lse_w.
-// o_w[d] is at op[w * o_stride + d], lse_w at lse[w * l_stride]. The loads go
-// out eight partials at a time with clamped indexes (weight 0 past the end),
-// so a many-way merge is not a chain of dependent load latencies.
+// Merge of n partials (o_w, lse_w), w = 0 .. n-1, into one output head, by
+// one wave: out[d] = sum_w 2^(lse_w - M) o_w[d] / sum_w 2^(lse_w - M),
+// M = max_w lse_w. o_w[d] is at op[w * o_stride + d] (16-byte aligned rows),
+// lse_w at lse[w * l_stride]; head_dim is a power of two from 16 to 256.
+//
+// Lane l reads 16 bytes (dims 4c .. 4c+3, c = l mod C, C = head_dim / 4) of
+// partial rows l / C, l / C + R, ... (R = 64 / C rows per wave-wide load),
+// up to kG rows per lane per round, each with its lse. The first round's loads go
+// out before the lse loads of the max and the sum, so for up to kG * R
+// partials (32 at head_dim 128) the merge waits for memory once. Indexes are
+// clamped (weight 0 past the end); rows are then summed across the R lane
+// groups with xor shuffles.
 template <typename E>
 __device__ __forceinline__ void merge_partials(const float* lse, int64_t l_stride, const float* op,
                                                int64_t o_stride, int n, int head_dim, typename E::S* out);
@@ -972,28 +989,50 @@ __device__ __forceinline__ float wave_max(float v) {
 template <typename E>
 __device__ __forceinline__ void merge_partials(const float* lse, int64_t l_stride, const float* op,
                                                int64_t o_stride, int n, int head_dim, typename E::S* out) {
-  constexpr int U = 8;
+  constexpr int kG = 16;
   const int lane = __lane_id();
+  const int cpr = head_dim >> 2;      // 16-byte chunks per row (4 .. 64)
+  const int rpl = 64 / cpr;           // rows per wave-wide load
+  const int c = lane & (cpr - 1);
+  const int r = lane / cpr;
+  f32x4 v[kG];
+  float lw[kG];
+  auto load_round = [&](int base) {
+#pragma unroll
+    for (int j = 0; j < kG; ++j) {
+      v[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      lw[j] = -INFINITY;
+      if (base + rpl * j < n) {  // wave-uniform: some lane has a row here
+        const int w = min(base + r + rpl * j, n - 1);
+        v[j] = *reinterpret_cast<const f32x4*>(op + w * o_stride + 4 * c);
+        lw[j] = lse[w * l_stride];
+      }
+    }
+  };
+  load_round(0);
   float mx = -INFINITY;
   for (int w = lane; w < n; w += 64) mx = fmaxf(mx, lse[w * l_stride]);
   mx = wave_max(mx);
   float den = 0.0f;
   for (int w = lane; w < n; w += 64) den += exp2f(lse[w * l_stride] - mx);
   den = wave_sum(den);
-  for (int d = lane; d < head_dim; d += 64) {
-    float num = 0.0f;
-    for (int w0 = 0; w0 < n; w0 += U) {
-      float wt[U], v[U];
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int per_round = kG * rpl;
+  for (int base = 0; base < n; base += per_round) {
+    if (base > 0) load_round(base);
 #pragma unroll
-      for (int j = 0; j < U; ++j) {
-        const int w = min(w0 + j, n - 1);
-        wt[j] = lse[w * l_stride];
-        v[j] = op[w * o_stride + d];
-      }
-#pragma unroll
-      for (int j = 0; j < U; ++j) num += (w0 + j < n ? exp2f(wt[j] - mx) : 0.0f) * v[j];
+    for (int j = 0; j < kG; ++j) {
+      const float wt = base + r + rpl * j < n ? exp2f(lw[j] - mx) : 0.0f;
+      acc += wt * v[j];
     }
-    out[d] = E::from_f32(num / den);
+  }
+  for (int off = cpr; off < 64; off <<= 1) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc[k] += __shfl_xor(acc[k], off, 64);
+  }
+  if (r == 0) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) out[4 * c + k] = E::from_f32(acc[k] / den);
   }
 }
 
@@ -1037,15 +1076,15 @@ __global__ void __launch_bounds__(64) decode_merge_balanced_kernel(const DecodeA
   const int hg = hl / a.heads_per_wg;
   const int hloc = hl % a.heads_per_wg;
   const int hp = a.num_kv_heads * a.head_groups;
-  const int n = seq_pages_uniform(a, b);
+  int64_t total, base;  // list length; list position of sequence b's first unit
+  int n;                // sequence b's pages
+  list_prefix(a, hp, b, &total, &base, &n);
   S* out = static_cast<S*>(a.out) + (static_cast<int64_t>(b) * a.num_q_heads + head) * head_dim;
   if (n == 0) {
     // No cached token: the softmax-weighted sum over no values is zero.
     for (int d = lane; d < head_dim; d += 64) out[d] = E::from_f32(0.0f);
     return;
   }
-  int64_t total, base;  // list length; list position of sequence b's first unit
-  list_prefix(a, hp, b, &total, &base);
   const int64_t per = balanced_per(a, total);
   const int r = kvh * a.head_groups + hg;
   const int64_t unit_base = base + static_cast<int64_t>(r) * n;
@@ -1243,7 +1282,7 @@ int make_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads, int 
     // Requested, or fewer units than CUs: pages balanced across sequences on the device.
     const int64_t upper = units * pages;  // list length if every sequence were full
     const int64_t grid = std::max<int64_t>(
-        1, std::min<int64_t>({cdiv(upper, kMinPagesPerSplit),
+        1, std::min<int64_t>({cdiv(upper, kMinPagesPerBalancedWg),
                               std::max<int64_t>(static_cast<int64_t>(cus) * kBalancedWgPerCu, units), 0x7fffffffLL}));
     p->grid = static_cast<int>(grid);
     p->num_splits = 0;
