@@ -15,9 +15,11 @@
 //                    a long sequence among short ones is spread over many
 //                    workgroups (chosen when units do not fill the device, or
 //                    on request).
-// A workgroup has four waves; a segment's 16-token blocks go round-robin to
-// the waves, each wave keeps its own running max / normaliser / output, and
-// the waves merge through LDS at the end. A segment that covers its whole unit
+// A segment runs on four waves; its 16-token blocks go round-robin to the
+// waves, each wave keeps its own running max / normaliser / output, and the
+// waves merge through LDS at the end. Uniform splits on a device they fill
+// twice over run two segments per 8-wave workgroup, KV heads 2j and 2j+1 of
+// one sequence side by side (adjacent bytes of every token row). A segment that covers its whole unit
 // writes the final output; otherwise it writes an fp32 partial output and its
 // log2-sum-exp, and a merge kernel combines the partials of each (sequence,
 // query head).
@@ -82,6 +84,9 @@ namespace {
 #ifndef KL_DECODE_XCD_REMAP
 #define KL_DECODE_XCD_REMAP 0  // give each XCD a contiguous range of work units
 #endif
+#ifndef KL_DECODE_PAIRED
+#define KL_DECODE_PAIRED 1  // two adjacent KV heads per 8-wave workgroup where the pairs fill the device
+#endif
 #ifndef KL_DECODE_KV_POLICY
 #define KL_DECODE_KV_POLICY kCachePolicyNT  // cache-policy bits of the K/V loads
 #endif
@@ -128,6 +133,7 @@ struct DecodeArgs {
   int q_fold;
   int q_heads;
   int force_partial;    // write fp32 partials (o, lse) even with one split
+  int paired;           // host only: uniform splits run two units per workgroup (decode_mfma_paired_kernel)
 };
 
 struct Unit {
@@ -148,6 +154,17 @@ __device__ __forceinline__ int xcd_remap(int pid, int n) {
   return xcd < tall ? xcd * per + local : tall * per + (xcd - tall) * (per - 1) + local;
 }
 
+// The sequence length and this split's page range of a unit whose b and
+// split are set.
+__device__ __forceinline__ void unit_pages(const DecodeArgs& a, Unit& u) {
+  const int raw = as_constant(a.seq_lens)[u.b];
+  const int64_t cap = static_cast<int64_t>(a.max_pages) * a.page_size;
+  u.seq_len = static_cast<int>(raw < cap ? raw : cap);
+  const int num_pages = u.seq_len > 0 ? (u.seq_len + a.page_size - 1) / a.page_size : 0;
+  u.page_begin = u.split * a.pages_per_split;
+  u.page_end = min(u.page_begin + a.pages_per_split, num_pages);
+}
+
 __device__ __forceinline__ Unit decode_unit(const DecodeArgs& a) {
   Unit u;
   int idx = KL_DECODE_XCD_REMAP ? xcd_remap(blockIdx.x, gridDim.x) : static_cast<int>(blockIdx.x);
@@ -157,24 +174,38 @@ __device__ __forceinline__ Unit decode_unit(const DecodeArgs& a) {
   idx /= a.head_groups;
   u.kvh = idx % a.num_kv_heads;
   u.b = idx / a.num_kv_heads;
-  const int raw = as_constant(a.seq_lens)[u.b];
-  const int64_t cap = static_cast<int64_t>(a.max_pages) * a.page_size;
-  u.seq_len = static_cast<int>(raw < cap ? raw : cap);
-  const int num_pages = u.seq_len > 0 ? (u.seq_len + a.page_size - 1) / a.page_size : 0;
-  u.page_begin = u.split * a.pages_per_split;
-  u.page_end = min(u.page_begin + a.pages_per_split, num_pages);
+  unit_pages(a, u);
+  return u;
+}
+
+// Paired workgroups (num_kv_heads even): workgroup i holds the units of KV
+// heads 2j and 2j+1 of one (sequence, head group, split), half `half`
+// taking KV head 2j + half. The digits of i are split (fastest), head
+// group, KV-head pair j, sequence.
+__device__ __forceinline__ Unit decode_unit_paired(const DecodeArgs& a, int half) {
+  Unit u;
+  int idx = static_cast<int>(blockIdx.x);
+  u.split = idx % a.num_splits;
+  idx /= a.num_splits;
+  u.hg = idx % a.head_groups;
+  idx /= a.head_groups;
+  const int pairs = a.num_kv_heads / 2;
+  u.kvh = 2 * (idx % pairs) + half;
+  u.b = idx / pairs;
+  unit_pages(a, u);
   return u;
 }
 
 // Writes zeros for the heads of an empty sequence (seq_len <= 0). The math of
 // kernel_lab/reference.py:58-67 gives zeros there (softmax over no tokens, then
 // an empty weighted sum).
+// Threads tid = 0 .. nthreads-1 of the unit's workgroup (or half) share the work.
 template <typename S, typename E>
-__device__ void write_zero_heads(const DecodeArgs& a, const Unit& u, int head_dim) {
+__device__ void write_zero_heads(const DecodeArgs& a, const Unit& u, int head_dim, int tid, int nthreads) {
   const int h0 = u.hg * a.heads_per_wg;
   const int nh = min(a.heads_per_wg, a.group - h0);
   S* out = static_cast<S*>(a.out);
-  for (int i = threadIdx.x; i < nh * head_dim; i += blockDim.x) {
+  for (int i = tid; i < nh * head_dim; i += nthreads) {
     const int h = u.kvh * a.group + h0 + i / head_dim;
     out[(static_cast<int64_t>(u.b) * a.num_q_heads + h) * head_dim + i % head_dim] = E::from_f32(0.0f);
   }
@@ -277,7 +308,8 @@ struct Dest {
 // into the score scale (K) and the epilogue (V): q.(s_k k) = s_k (q.k) and
 // sum p (s_v v) = s_v sum p v.
 template <typename E, typename KVF, int D, int NT>
-__device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, const Unit& u, const Dest& dst) {
+__device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, const Unit& u, const Dest& dst,
+                                             const int wave) {
   using S = typename E::S;
   using KS = typename KVF::S;          // cache storage type
   using M = Mfma<E>;
@@ -295,7 +327,6 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
   constexpr int NS = mfma_stages<D>();
 
   const int lane = __lane_id();
-  const int wave = wave_id();
   const int row = lane & 15;  // MFMA row / column index of this lane
   const int grp = lane >> 4;  // MFMA k-group of this lane
   const int h0 = u.hg * a.heads_per_wg;
@@ -576,6 +607,20 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
   }
 }
 
+// Output of a uniform-split unit: the final output with one split, else its
+// split's slot of o_part [batch, num_q_heads, num_splits, head_dim] and
+// lse_part [batch, num_q_heads, num_splits].
+__device__ __forceinline__ Dest uniform_dest(const DecodeArgs& a, const Unit& u, int head_dim) {
+  Dest dst;
+  dst.final = a.num_splits == 1 && !a.force_partial;
+  const int64_t head0 = static_cast<int64_t>(u.b) * a.num_q_heads + u.kvh * a.group + u.hg * a.heads_per_wg;
+  dst.o = dst.final ? nullptr : a.o_part + (head0 * a.num_splits + u.split) * head_dim;
+  dst.lse = dst.final ? nullptr : a.lse_part + head0 * a.num_splits + u.split;
+  dst.o_head_stride = static_cast<int64_t>(a.num_splits) * head_dim;
+  dst.lse_head_stride = a.num_splits;
+  return dst;
+}
+
 // Uniform splits: workgroup = (sequence, KV head, head group, split), the
 // split owning pages_per_split pages (the reference's decomposition).
 template <typename E, typename KVF, int D, int NT>
@@ -584,18 +629,40 @@ __global__ void __launch_bounds__(kThreads, (mfma_waves_per_eu<D, NT>())) decode
   const Unit u = decode_unit(a);
   if (u.page_begin >= u.page_end) {
     if (u.split == 0 && u.seq_len <= 0 && a.num_splits == 1 && !a.force_partial) {
-      write_zero_heads<typename E::S, E>(a, u, D);
+      write_zero_heads<typename E::S, E>(a, u, D, threadIdx.x, blockDim.x);
     }
     return;  // a split past the end of its sequence has no work
   }
-  Dest dst;
-  dst.final = a.num_splits == 1 && !a.force_partial;
-  const int64_t head0 = static_cast<int64_t>(u.b) * a.num_q_heads + u.kvh * a.group + u.hg * a.heads_per_wg;
-  dst.o = dst.final ? nullptr : a.o_part + (head0 * a.num_splits + u.split) * D;
-  dst.lse = dst.final ? nullptr : a.lse_part + head0 * a.num_splits + u.split;
-  dst.o_head_stride = static_cast<int64_t>(a.num_splits) * D;
-  dst.lse_head_stride = a.num_splits;
-  mfma_segment<E, KVF, D, NT>(a, lds, u, dst);
+  mfma_segment<E, KVF, D, NT>(a, lds, u, uniform_dest(a, u, D), wave_id());
+}
+
+// Uniform splits, two units per 8-wave workgroup: waves 0-3 take KV head 2j
+// and waves 4-7 KV head 2j+1 of the same sequence, head group and split
+// (decode_unit_paired), each half with its own LDS. The two halves run the
+// same segment code as decode_mfma_kernel; together they read 2 adjacent
+// head slices (512 contiguous bytes at head_dim 128, 16-bit) of every token
+// row at about the same time. Measured on MI355X with the decode's own
+// gather as pure loads (B=64, 32/8/128/16 fp16): 6.8 TB/s against 6.5 TB/s
+// for one head per 4-wave workgroup; pairing two sequences' units instead
+// gains nothing, so the gain is the adjacent-head locality, not the larger
+// workgroup.
+template <typename E, typename KVF, int D, int NT>
+__global__ void __launch_bounds__(2 * kThreads, (mfma_waves_per_eu<D, NT>()))
+    decode_mfma_paired_kernel(const DecodeArgs a) {
+  __shared__ __attribute__((aligned(16))) char lds[2 * MfmaLds<D, NT>::kBytes];
+  const int wave = wave_id();
+  const int half = wave / kWaves;
+  const Unit u = decode_unit_paired(a, half);
+  if (u.page_begin >= u.page_end) {
+    // The other half's segment passes two workgroup barriers: pass them too.
+    __syncthreads();
+    __syncthreads();
+    if (u.split == 0 && u.seq_len <= 0 && a.num_splits == 1 && !a.force_partial) {
+      write_zero_heads<typename E::S, E>(a, u, D, threadIdx.x - half * kThreads, kThreads);
+    }
+    return;
+  }
+  mfma_segment<E, KVF, D, NT>(a, lds + half * MfmaLds<D, NT>::kBytes, u, uniform_dest(a, u, D), wave - half * kWaves);
 }
 
 // ------------------------------------------------------- balanced schedule
@@ -767,7 +834,7 @@ __global__ void __launch_bounds__(kThreads, (mfma_waves_per_eu<D, NT>()))
     dst.lse_head_stride = 1;
 
     __syncthreads();  // the previous segment's wave 0 may still read LDS
-    mfma_segment<E, KVF, D, NT>(a, lds, u, dst);
+    mfma_segment<E, KVF, D, NT>(a, lds, u, dst, wave_id());
 
     pos = unit_base + page1;
     if (r == hp - 1 && page1 == n) {  // this sequence's units are done: next non-empty one
@@ -826,7 +893,9 @@ __global__ void __launch_bounds__(kThreads) decode_valu_kernel(const DecodeArgs 
 
   const Unit u = decode_unit(a);
   if (u.page_begin >= u.page_end) {
-    if (u.split == 0 && u.seq_len <= 0 && a.num_splits == 1) write_zero_heads<typename E::S, E>(a, u, D);
+    if (u.split == 0 && u.seq_len <= 0 && a.num_splits == 1) {
+      write_zero_heads<typename E::S, E>(a, u, D, threadIdx.x, blockDim.x);
+    }
     return;
   }
   const int lane = __lane_id();
@@ -1204,6 +1273,13 @@ bool valu_forced() {
   return v != nullptr && v[0] == '1';
 }
 
+// KL_DECODE_PAIRED=0 turns paired workgroups off (for A/B measurements).
+bool pairing_enabled() {
+  if (!KL_DECODE_PAIRED) return false;
+  const char* v = std::getenv("KL_DECODE_PAIRED");
+  return v == nullptr || v[0] != '0';
+}
+
 bool valu_head_dim_ok(kl_dtype dtype, int head_dim) {
   const int vec = dtype == KL_DTYPE_F32 ? 4 : 8;
   switch (head_dim) {
@@ -1241,6 +1317,7 @@ struct Plan {
   int heads_per_wg;
   int head_groups;
   int grid;             // balanced-schedule workgroups; 0 for uniform splits
+  bool paired;          // uniform splits: two adjacent KV heads per 8-wave workgroup
   size_t o_bytes;
   size_t ws_bytes;
 };
@@ -1275,6 +1352,7 @@ int make_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads, int 
   head_tiling(mfma, head_dim, group, &p->heads_per_wg, &p->head_groups);
   const int pages = std::max(max_pages, 1);
   p->grid = 0;
+  p->paired = false;
   const int cus = cu_count > 0 ? cu_count : 256;
   const int64_t units = std::max<int64_t>(1, static_cast<int64_t>(batch) * num_kv_heads * p->head_groups);
   if (num_splits == KL_SPLITS_BALANCED && (!mfma || partials)) num_splits = 0;  // uniform splits only
@@ -1309,6 +1387,10 @@ int make_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads, int 
   s = static_cast<int>(cdiv(pages, pps));
   p->num_splits = s;
   p->pages_per_split = pps;
+  // Two adjacent KV heads per 8-wave workgroup when the pairs alone give
+  // every CU a workgroup (one 8-wave workgroup per CU is the register budget)
+  // and the 4-wave kernel fits two waves per SIMD (head_dim <= 128).
+  p->paired = mfma && pairing_enabled() && num_kv_heads % 2 == 0 && head_dim <= 128 && units * s / 2 >= cus;
   if (s > 1 || partials) {
     const size_t rows = static_cast<size_t>(batch) * num_q_heads * s;
     p->o_bytes = align_up(rows * head_dim * sizeof(float));
@@ -1381,12 +1463,27 @@ int launch_valu(const DecodeArgs& a, int head_dim, unsigned grid, hipStream_t st
   return fail(KL_ERR_UNSUPPORTED, "no kernel for this head_dim");
 }
 
+// grid: the number of units (sequences x KV heads x head groups x splits);
+// paired launches take two units per workgroup, so grid must then be even.
 template <typename E, typename KVF>
 int launch_uniform_mfma(const DecodeArgs& a, int head_dim, unsigned grid, hipStream_t stream) {
+  if (a.paired && (grid % 2 != 0 || a.num_kv_heads % 2 != 0)) {
+    return fail(KL_ERR_UNSUPPORTED, "paired decode launch needs an even number of KV heads");
+  }
   return dispatch_mfma(head_dim, a.heads_per_wg, [&](auto d, auto nt) -> int {
     constexpr int D = decltype(d)::value, NT = decltype(nt)::value;
     if constexpr (mfma_instance_exists<KVF, D>()) {
-      decode_mfma_kernel<E, KVF, D, NT><<<grid, kThreads, 0, stream>>>(a);
+      if (a.paired) {
+        // head_dim 256 is never paired: its segment needs more than the
+        // 256 registers per lane an 8-wave workgroup leaves.
+        if constexpr (D <= 128) {
+          decode_mfma_paired_kernel<E, KVF, D, NT><<<grid / 2, 2 * kThreads, 0, stream>>>(a);
+        } else {
+          return fail(KL_ERR_UNSUPPORTED, "paired decode needs head_dim <= 128");
+        }
+      } else {
+        decode_mfma_kernel<E, KVF, D, NT><<<grid, kThreads, 0, stream>>>(a);
+      }
       return KL_OK;
     } else {
       return fail(KL_ERR_UNSUPPORTED, "an FP8 cache needs head_dim 64, 128 or 256");
@@ -1535,6 +1632,7 @@ int decode_entry(kl_dtype dtype, bool kv8, void* out, const void* q, const void*
   a.q_fold = a.group;
   a.q_heads = num_q_heads;
   a.force_partial = 0;
+  a.paired = p.paired ? 1 : 0;
 
   const bool mfma = use_mfma && mfma_path(dtype, head_dim, page_size);
   switch (dtype) {
@@ -1636,6 +1734,7 @@ int cascade_launch(const DecodeArgs& base, const CascadePlan& cp, const int32_t*
     a.heads_per_wg = cp.pre.heads_per_wg;
     a.o_part = reinterpret_cast<float*>(ws);
     a.lse_part = reinterpret_cast<float*>(ws + cp.pre.o_bytes);
+    a.paired = cp.pre.paired ? 1 : 0;
     const int64_t wgs = static_cast<int64_t>(a.num_kv_heads) * a.head_groups * a.num_splits;
     if (wgs > 0x7fffffffLL) return fail(KL_ERR_UNSUPPORTED, "too many workgroups");
     int st = launch_uniform_mfma<E, E>(a, head_dim, static_cast<unsigned>(wgs), stream);
@@ -1654,6 +1753,7 @@ int cascade_launch(const DecodeArgs& base, const CascadePlan& cp, const int32_t*
   a.heads_per_wg = cp.suf.heads_per_wg;
   a.o_part = reinterpret_cast<float*>(ws + cp.pre_bytes);
   a.lse_part = reinterpret_cast<float*>(ws + cp.pre_bytes + cp.suf.o_bytes);
+  a.paired = cp.suf.paired ? 1 : 0;
   const int64_t wgs = static_cast<int64_t>(batch) * a.num_kv_heads * a.head_groups * a.num_splits;
   if (wgs > 0x7fffffffLL) return fail(KL_ERR_UNSUPPORTED, "too many workgroups");
   int st = launch_uniform_mfma<E, E>(a, head_dim, static_cast<unsigned>(wgs), stream);
@@ -1747,6 +1847,7 @@ extern "C" int kl_cascade_decode_attention(kl_dtype dtype, void* out, const void
   a.group = num_q_heads / num_kv_heads;
   a.page_size = page_size;
   a.grid = 0;
+  a.paired = 0;
   a.scale_log2 = scale * kLog2e;
   a.q_fold = a.group;
   a.q_heads = num_q_heads;

@@ -1,0 +1,104 @@
+"""Paired decode workgroups (two adjacent KV heads per 8-wave workgroup).
+
+The planner pairs the units of KV heads 2j and 2j+1 of one sequence, head
+group and split into one workgroup when the KV head count is even, head_dim
+is at most 128 and the pairs alone give each of MI355X's 256 CUs a workgroup
+(sequences x KV heads x head groups x splits >= 512). Each half runs the same
+segment code over the same blocks as the one-unit workgroup, so the output
+must be bit-identical with pairing switched off (``KL_DECODE_PAIRED=0``) and
+match the oracle. The shapes below all pair on MI355X; they cover one split
+(final outputs written by each half), requested splits with splits past the
+end of short sequences (both halves empty), empty sequences (zeros), two head
+tiles per workgroup (GQA group 24), head_dim 32 and 64, and the FP8 cache.
+"""
+
+from __future__ import annotations
+
+import os
+
+import pytest
+import torch
+
+from kernel_lab.kv_cache import quantize_fp8, random_decode_problem
+from oracle import reference as ref
+from tests.conftest import tolerance
+
+pytestmark = pytest.mark.gpu
+
+
+def _lens(batch: int, hi: int, seed: int) -> list[int]:
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(1, hi + 1, (batch,), generator=g).tolist()
+
+
+def _empty_rows(batch: int, empty: int) -> list[int]:
+    return sorted({(7 * i + 3) % batch for i in range(empty)})
+
+
+def _both(ops, q, kv, **kw):
+    """The decode with pairing as planned and with pairing switched off."""
+    paired = ops.paged_decode_attention(q, kv.k_cache, kv.v_cache, kv.block_table, kv.seq_lens, **kw)
+    old = os.environ.get("KL_DECODE_PAIRED")
+    os.environ["KL_DECODE_PAIRED"] = "0"
+    try:
+        single = ops.paged_decode_attention(q, kv.k_cache, kv.v_cache, kv.block_table, kv.seq_lens, **kw)
+    finally:
+        if old is None:
+            del os.environ["KL_DECODE_PAIRED"]
+        else:
+            os.environ["KL_DECODE_PAIRED"] = old
+    torch.cuda.synchronize()
+    return paired.cpu(), single.cpu()
+
+
+CASES = [
+    # (batch, hq, hkv, head_dim, dtype, max_len, num_splits, empty sequences)
+    (64, 32, 8, 128, torch.float16, 700, None, 0),
+    (64, 32, 8, 128, torch.bfloat16, 500, None, 5),
+    (8, 32, 8, 128, torch.float16, 900, 16, 0),
+    (16, 16, 4, 128, torch.bfloat16, 600, 64, 2),
+    (64, 192, 8, 128, torch.float16, 200, None, 0),
+    (128, 16, 4, 64, torch.float16, 300, None, 3),
+    (64, 32, 8, 32, torch.bfloat16, 400, 2, 0),
+]
+
+
+@pytest.mark.parametrize(("batch", "hq", "hkv", "head_dim", "dtype", "max_len", "num_splits", "empty"), CASES)
+def test_paired_matches_unpaired_and_oracle(gpu_ops, batch, hq, hkv, head_dim, dtype, max_len, num_splits, empty):
+    lens = _lens(batch, max_len, seed=batch + hq + head_dim)
+    q, kv, _, _ = random_decode_problem(lens, hq, hkv, head_dim, 16, dtype=dtype, device="cuda", poison=float("nan"))
+    empties = _empty_rows(batch, empty)
+    kv.seq_lens[empties] = 0  # the fixture needs a token per sequence; these attend over none
+    kw = {} if num_splits is None else {"num_splits": num_splits}
+    paired, single = _both(gpu_ops, q, kv, **kw)
+    assert torch.isfinite(paired).all(), "non-finite output: a poisoned page or tail leaked in"
+    assert torch.equal(paired, single), "paired workgroups changed the result"
+    want = ref.paged_decode_attention(
+        q.cpu(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table.cpu(), kv.seq_lens.cpu()
+    )
+    torch.testing.assert_close(paired, want, **tolerance(dtype))
+    for b in empties:
+        assert not paired[b].any(), "an empty sequence must give zeros"
+
+
+def test_paired_fp8_cache_matches_unpaired(gpu_ops):
+    lens = _lens(64, 600, seed=11)
+    q, kv, _, _ = random_decode_problem(lens, 32, 8, 128, 16, dtype=torch.float16, device="cuda", poison=float("nan"))
+    kv8, ks, vs = quantize_fp8(kv)
+    k8, v8 = kv8.k_cache, kv8.v_cache
+    args = (q, k8, v8, kv.block_table, kv.seq_lens)
+    paired = gpu_ops.paged_decode_attention(*args, k_scale=ks, v_scale=vs)
+    old = os.environ.get("KL_DECODE_PAIRED")
+    os.environ["KL_DECODE_PAIRED"] = "0"
+    try:
+        single = gpu_ops.paged_decode_attention(*args, k_scale=ks, v_scale=vs)
+    finally:
+        if old is None:
+            del os.environ["KL_DECODE_PAIRED"]
+        else:
+            os.environ["KL_DECODE_PAIRED"] = old
+    assert torch.equal(paired.cpu(), single.cpu()), "paired workgroups changed the FP8 result"
+    want = ref.paged_decode_attention_fp8(
+        q.cpu(), k8.cpu(), v8.cpu(), kv.block_table.cpu(), kv.seq_lens.cpu(), ks.cpu(), vs.cpu()
+    )
+    torch.testing.assert_close(paired.cpu(), want, **tolerance(torch.float16))
