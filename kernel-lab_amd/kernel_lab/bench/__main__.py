@@ -8,8 +8,8 @@ the measured configurations):
 * rmsnorm: fused add+RMSNorm at tokens {1, 16, 128, 1024, 4096} x hidden
   {4096, 8192};
 * decode: Llama-3-8B GQA (32/8/128/16) at batch {1, 8, 32, 64} x context
-  {512, 4096} with the planner and with fixed splits; ragged-length MQA
-  (32/1/128, batch 64, L ~ U[1, 8192]); long-context 70B-style GQA
+  {512, 4096} with the planner and with fixed splits; ragged-length MQA and
+  GQA (32/1/128 and 32/8/128, batch 64, L ~ U[1, 8192]); long-context 70B-style GQA
   (64/8/128, batch 8, contexts 32768 and 131072);
 * decode-fp8: the FP8 (E4M3) cache against a 16-bit cache holding the same
   values, at the headline, ragged and long-context shapes;
@@ -210,6 +210,7 @@ def decode_cases(dtype: torch.dtype) -> list[tuple[str, list[int], int, int, tor
     g = torch.Generator().manual_seed(3)
     ragged = torch.randint(1, 8193, (64,), generator=g).tolist()
     cases.append(("32/1/128 b64 ragged U[1,8192]", ragged, 32, 1, torch.bfloat16 if dtype != torch.float32 else dtype))
+    cases.append(("32/8/128 b64 ragged U[1,8192]", ragged, 32, 8, dtype))
     # One long sequence among short ones: splits sized from the block table's
     # width leave most of the work to the long sequence's few workgroups.
     cases.append(("32/8/128 b16 skewed 1x65536+15x1024", [65536] + [1024] * 15, 32, 8, dtype))
@@ -227,6 +228,16 @@ def _forced_valu(fn: Callable[[], torch.Tensor]) -> torch.Tensor:
         return fn()
     finally:
         del os.environ["KL_DECODE_FORCE_VALU"]
+
+
+def _unpaired(fn: Callable[[], torch.Tensor]) -> torch.Tensor:
+    """Runs fn with paired workgroups (two adjacent KV heads per 8-wave
+    workgroup) switched off (KL_DECODE_PAIRED=0, read on every call)."""
+    os.environ["KL_DECODE_PAIRED"] = "0"
+    try:
+        return fn()
+    finally:
+        del os.environ["KL_DECODE_PAIRED"]
 
 
 def decode_suite(
@@ -256,6 +267,10 @@ def decode_suite(
             impls["torch (gather + matmul)"] = lambda a=args, s=scale: torch_paged_decode(*a, s)
         impls["hip split-KV (planner)"] = lambda a=args, s=scale, o=out: ops.paged_decode_attention(*a, s, out=o)
         if dt != torch.float32:
+            if hkv % 2 == 0:
+                impls["hip unpaired (planner)"] = lambda a=args, s=scale, o=out2: _unpaired(
+                    lambda: ops.paged_decode_attention(*a, s, out=o)
+                )
             impls["hip VALU kernel (planner)"] = lambda a=args, s=scale, o=out2: _forced_valu(
                 lambda: ops.paged_decode_attention(*a, s, out=o)
             )
@@ -308,6 +323,10 @@ def decode_fp8_suite(peak: GPUPeak | None, timer, shape: str | None = None) -> l
             ),
             "hip fp8 cache (planner)": lambda: ops.paged_decode_attention(*a8, scale, out=out8, k_scale=ks, v_scale=vs),
         }
+        if hkv % 2 == 0:
+            impls["hip fp8 cache unpaired (planner)"] = lambda: _unpaired(
+                lambda: ops.paged_decode_attention(*a8, scale, out=out8, k_scale=ks, v_scale=vs)
+            )
         w16 = decode_attention_work(lens, hq, hkv, d, 2)
         w8 = decode_attention_work(lens, hq, hkv, d, 2, kv_elem_bytes=1)
         work = {name: (w8 if "fp8" in name else w16) for name in impls}
