@@ -121,6 +121,16 @@ int kl_paged_decode_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_
  * suits batches of very uneven lengths. The workspace must hold at least
  * the bytes kl_paged_decode_plan reports for the same arguments; it may be
  * NULL when that is 0. batch == 0 is a successful no-op.
+ *
+ * Split sequences are merged inside the decode kernel where the path allows
+ * it (fp16/bf16, at most 8 query heads per KV head and head group): the
+ * library keeps per-device arrival counters (512 KiB) in 16 regions, each
+ * taken by the first stream that needs one and reused by that stream's later
+ * calls, which the stream runs one after another. A call on a stream beyond
+ * the 16 falls back to a separate merge launch; results are bit-identical
+ * either way. KL_DECODE_FUSED_MERGE=0 in the environment forces the merge
+ * launch. A captured graph keeps the region of the stream it was captured on:
+ * replaying it on another stream while that stream runs decode calls races.
  */
 int kl_paged_decode_attention(kl_dtype dtype, void* out, const void* q, const void* k_cache,
                               const void* v_cache, const int32_t* block_table,

@@ -187,14 +187,59 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
                                            kBufferDword3);
 }
 
+// A pointer that is the same in every lane, made provably wave-uniform
+// (scalar registers), so a buffer resource built from it stays scalar; built
+// from a per-lane value, every buffer access becomes a per-lane loop.
+template <typename T>
+__device__ __forceinline__ T* uniform_ptr(T* p) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32));
+  return reinterpret_cast<T*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 // Cache-policy bits of the buffer instruction (gfx940+ encoding): NT marks a
 // streaming access, which measured ~13% more HBM read bandwidth than the
 // default policy for data read once.
 constexpr int kCachePolicyNT = 2;
 
+// Device-scope coherence (the sc1 bit): a store is written through to where
+// every XCD sees it and a load does not return a line another XCD may have
+// changed. It is the encoding this compiler gives relaxed agent-scope atomic
+// loads and stores on gfx950, used here for plain data that workgroups on
+// different XCDs exchange within one launch, without the whole-L2 write-back
+// and invalidate of an agent-scope fence.
+constexpr int kCachePolicyDevice = 16;
+
 template <int POLICY = 0>
 __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t byte_offset) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, byte_offset, 0, POLICY));
+}
+
+template <int POLICY = 0>
+__device__ __forceinline__ float buffer_load_f32(__amdgpu_buffer_rsrc_t rsrc, uint32_t byte_offset) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, byte_offset, 0, POLICY));
+}
+
+template <int POLICY = 0>
+__device__ __forceinline__ void buffer_store16(__amdgpu_buffer_rsrc_t rsrc, uint32_t byte_offset, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, rsrc, byte_offset, 0, POLICY);
+}
+
+template <int POLICY = 0>
+__device__ __forceinline__ void buffer_store_f32(__amdgpu_buffer_rsrc_t rsrc, uint32_t byte_offset, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), rsrc, byte_offset, 0, POLICY);
+}
+
+// Waits until every vector memory access this wave issued has completed
+// (s_waitcnt vmcnt(0); gfx9 counts stores there too). After device-scope
+// stores it orders them before a following device-scope atomic, which is
+// what a release needs when no ordinary store has to be written back. The
+// signal fences keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void wait_vector_memory() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt and lgkmcnt unconstrained
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 // gfx950 transposing LDS read (ds_read_b64_tr_b16). Within each 16-lane row,

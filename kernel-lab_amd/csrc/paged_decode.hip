@@ -48,6 +48,8 @@
 #include <algorithm>
 #include <cstdlib>
 #include <cmath>
+#include <mutex>
+#include <vector>
 #include <type_traits>
 
 #include "hip_common.h"
@@ -86,6 +88,9 @@ namespace {
 #endif
 #ifndef KL_DECODE_PAIRED
 #define KL_DECODE_PAIRED 1  // two adjacent KV heads per 8-wave workgroup where the pairs fill the device
+#endif
+#ifndef KL_DECODE_FUSED_MERGE
+#define KL_DECODE_FUSED_MERGE 1  // the last segment of a split unit merges it (no merge kernel)
 #endif
 #ifndef KL_DECODE_KV_POLICY
 #define KL_DECODE_KV_POLICY kCachePolicyNT  // cache-policy bits of the K/V loads
@@ -134,6 +139,9 @@ struct DecodeArgs {
   int q_heads;
   int force_partial;    // write fp32 partials (o, lse) even with one split
   int paired;           // host only: uniform splits run two units per workgroup (decode_mfma_paired_kernel)
+  // Fused merge: this call's arrival counters, one per unit, zero on entry
+  // and left zero (null: a merge kernel combines the partials).
+  uint32_t* arrivals;
 };
 
 struct Unit {
@@ -599,20 +607,132 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
         S* out = static_cast<S*>(a.out) + head * D + d;
         *reinterpret_cast<u32x2*>(out) = u32x2{pack2<E>(o[0], o[1]), pack2<E>(o[2], o[3])};
       } else {
-        float* op = dst.o + static_cast<int64_t>(16 * t + row) * dst.o_head_stride + d;
-        *reinterpret_cast<f32x4*>(op) = f32x4{o[0], o[1], o[2], o[3]};
+        // Partials are stored device-coherent: with the fused merge, a
+        // workgroup on another XCD reads them within this launch.
+        const uint32_t off = static_cast<uint32_t>((static_cast<int64_t>(16 * t + row) * dst.o_head_stride + d) * 4);
+        buffer_store16<kCachePolicyDevice>(make_rsrc(uniform_ptr(dst.o)), off,
+                                           __builtin_bit_cast(u32x4, f32x4{o[0], o[1], o[2], o[3]}));
       }
     }
-    if (valid && !dst.final && grp == 0) dst.lse[(16 * t + row) * dst.lse_head_stride] = mmax + log2f(denom);
+    if (valid && !dst.final && grp == 0) {
+      buffer_store_f32<kCachePolicyDevice>(make_rsrc(uniform_ptr(dst.lse)),
+                                           static_cast<uint32_t>((16 * t + row) * dst.lse_head_stride * 4),
+                                           mmax + log2f(denom));
+    }
   }
+}
+
+// ------------------------------------------------------- fused split merge
+//
+// A unit split across several segments (uniform splits, or a balanced
+// workgroup range) is merged by whichever of its segments finishes last, in
+// the decode kernel itself, instead of by a separate merge launch (measured
+// at 4.0-5.5 us per call on MI355X). Each segment that wrote a partial
+// publishes it (release fence) and adds one to its unit's arrival counter;
+// the one that brings the counter to the unit's segment count resets it to
+// zero, acquires the others' partials and merges them with merge_partials,
+// so the result is bit-identical to the merge kernels'. Nobody waits, so a
+// missing arrival cannot hang a workgroup.
+//
+// The counters live in device memory owned by the library, zero when the
+// code object is loaded and zero again after every call. A call takes the
+// counters of a region that belongs to its stream (kernels on one stream
+// never overlap); with more streams than regions the call falls back to the
+// merge kernel.
+constexpr int kArrivalRegions = 16;      // streams served per device
+constexpr int kArrivalCounters = 8192;   // units per region
+constexpr int kFusedMergeMaxHeads = 8;   // query heads of a unit, merged one per wave
+
+__device__ uint32_t g_decode_arrivals[kArrivalRegions * kArrivalCounters];
+
+template <typename E, int kG = 16, int POL = 0>
+__device__ __forceinline__ void merge_partials(const float* lse, int64_t l_stride, const float* op,
+                                               int64_t o_stride, int n, int head_dim, typename E::S* out);
+
+// The partials of one unit: head hl's n partials (lse at lse + hl *
+// lse_head_stride + w * l_stride, rows at o + hl * o_head_stride + w *
+// o_stride) merge into out + hl * head_dim.
+struct MergeJob {
+  const float* lse;
+  int64_t lse_head_stride, l_stride;
+  const float* o;
+  int64_t o_head_stride, o_stride;
+  int n;      // partials per head (the unit's segments)
+  int heads;  // query heads of the unit
+  void* out;
+};
+
+// Called by every wave of the segment's four waves after a segment that
+// wrote a partial (wave 0 wrote it). One workgroup barrier, reached by every
+// wave of the workgroup: paired halves call it together.
+//
+// Release: wave 0 stored the partial device-coherent (sc1); waiting for those
+// stores to complete before the device-scope add makes them visible to
+// whoever sees the add. Acquire: the last arriver reads the partials with
+// device-coherent loads, issued only after the add returned.
+template <typename E>
+__device__ void arrive_and_merge(uint32_t* counter, const MergeJob& job, int head_dim, int wave, int* s_last) {
+  if (wave == 0) {
+    wait_vector_memory();
+    if (__lane_id() == 0) {
+      const uint32_t old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int last = old + 1 == static_cast<uint32_t>(job.n);
+      // Every arrival has happened: leave the counter zero for the next call.
+      if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *s_last = last;
+    }
+  }
+  __syncthreads();
+  const int last = __builtin_amdgcn_readfirstlane(*s_last);
+  if (!last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");  // no load moves above the arrival
+  using S = typename E::S;
+  for (int h = wave; h < job.heads; h += kWaves) {
+    // 4 rows per lane per round: a unit rarely has more than 8 segments, and
+    // the decode kernel's registers stay within its occupancy budget.
+    merge_partials<E, 4, kCachePolicyDevice>(job.lse + h * job.lse_head_stride, job.l_stride,
+                                             job.o + h * job.o_head_stride, job.o_stride, job.n, head_dim,
+                                             static_cast<S*>(job.out) + static_cast<int64_t>(h) * head_dim);
+  }
+}
+
+// Segments (splits with pages) of a uniform-split unit.
+__device__ __forceinline__ int active_splits(const DecodeArgs& a, const Unit& u) {
+  const int num_pages = u.seq_len > 0 ? (u.seq_len + a.page_size - 1) / a.page_size : 0;
+  return min(a.num_splits, (num_pages + a.pages_per_split - 1) / a.pages_per_split);
+}
+
+// The merge of a uniform-split unit: partial w is split w of the unit's heads
+// in o_part [batch, num_q_heads, num_splits, head_dim].
+template <typename E>
+__device__ __forceinline__ MergeJob uniform_job(const DecodeArgs& a, const Unit& u, int head_dim, int n) {
+  const int h0 = u.hg * a.heads_per_wg;
+  const int64_t head0 = static_cast<int64_t>(u.b) * a.num_q_heads + u.kvh * a.group + h0;
+  MergeJob j;
+  j.lse = a.lse_part + head0 * a.num_splits;
+  j.lse_head_stride = a.num_splits;
+  j.l_stride = 1;
+  j.o = a.o_part + head0 * a.num_splits * head_dim;
+  j.o_head_stride = static_cast<int64_t>(a.num_splits) * head_dim;
+  j.o_stride = head_dim;
+  j.n = n;
+  j.heads = min(a.heads_per_wg, a.group - h0);
+  j.out = static_cast<typename E::S*>(a.out) + head0 * head_dim;
+  return j;
+}
+
+__device__ __forceinline__ uint32_t* unit_counter(const DecodeArgs& a, const Unit& u) {
+  return a.arrivals + (static_cast<int64_t>(u.b) * a.num_kv_heads + u.kvh) * a.head_groups + u.hg;
 }
 
 // Output of a uniform-split unit: the final output with one split, else its
 // split's slot of o_part [batch, num_q_heads, num_splits, head_dim] and
 // lse_part [batch, num_q_heads, num_splits].
+// With the fused merge, a unit whose sequence reaches only one split writes
+// its output directly (bit-identical: a single partial merges to itself).
 __device__ __forceinline__ Dest uniform_dest(const DecodeArgs& a, const Unit& u, int head_dim) {
   Dest dst;
-  dst.final = a.num_splits == 1 && !a.force_partial;
+  dst.final = !a.force_partial && (a.num_splits == 1 || (a.arrivals != nullptr && active_splits(a, u) == 1));
   const int64_t head0 = static_cast<int64_t>(u.b) * a.num_q_heads + u.kvh * a.group + u.hg * a.heads_per_wg;
   dst.o = dst.final ? nullptr : a.o_part + (head0 * a.num_splits + u.split) * head_dim;
   dst.lse = dst.final ? nullptr : a.lse_part + head0 * a.num_splits + u.split;
@@ -626,14 +746,21 @@ __device__ __forceinline__ Dest uniform_dest(const DecodeArgs& a, const Unit& u,
 template <typename E, typename KVF, int D, int NT>
 __global__ void __launch_bounds__(kThreads, (mfma_waves_per_eu<D, NT>())) decode_mfma_kernel(const DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[MfmaLds<D, NT>::kBytes];
+  __shared__ int s_last[1];
   const Unit u = decode_unit(a);
   if (u.page_begin >= u.page_end) {
-    if (u.split == 0 && u.seq_len <= 0 && a.num_splits == 1 && !a.force_partial) {
+    if (u.split == 0 && u.seq_len <= 0 && (a.num_splits == 1 || a.arrivals != nullptr) && !a.force_partial) {
       write_zero_heads<typename E::S, E>(a, u, D, threadIdx.x, blockDim.x);
     }
     return;  // a split past the end of its sequence has no work
   }
-  mfma_segment<E, KVF, D, NT>(a, lds, u, uniform_dest(a, u, D), wave_id());
+  const Dest dst = uniform_dest(a, u, D);
+  mfma_segment<E, KVF, D, NT>(a, lds, u, dst, wave_id());
+  if constexpr (NT == 1) {  // the fused merge takes units of at most kFusedMergeMaxHeads heads
+    if (!dst.final && a.arrivals != nullptr) {
+      arrive_and_merge<E>(unit_counter(a, u), uniform_job<E>(a, u, D, active_splits(a, u)), D, wave_id(), s_last);
+    }
+  }
 }
 
 // Uniform splits, two units per 8-wave workgroup: waves 0-3 take KV head 2j
@@ -650,19 +777,30 @@ template <typename E, typename KVF, int D, int NT>
 __global__ void __launch_bounds__(2 * kThreads, (mfma_waves_per_eu<D, NT>()))
     decode_mfma_paired_kernel(const DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[2 * MfmaLds<D, NT>::kBytes];
+  __shared__ int s_last[2];
   const int wave = wave_id();
   const int half = wave / kWaves;
+  // Both halves hold the same sequence and split, so they agree on whether
+  // there is work, whether it is final and how many segments the unit has:
+  // they pass the same workgroup barriers.
   const Unit u = decode_unit_paired(a, half);
   if (u.page_begin >= u.page_end) {
     // The other half's segment passes two workgroup barriers: pass them too.
     __syncthreads();
     __syncthreads();
-    if (u.split == 0 && u.seq_len <= 0 && a.num_splits == 1 && !a.force_partial) {
+    if (u.split == 0 && u.seq_len <= 0 && (a.num_splits == 1 || a.arrivals != nullptr) && !a.force_partial) {
       write_zero_heads<typename E::S, E>(a, u, D, threadIdx.x - half * kThreads, kThreads);
     }
     return;
   }
-  mfma_segment<E, KVF, D, NT>(a, lds + half * MfmaLds<D, NT>::kBytes, u, uniform_dest(a, u, D), wave - half * kWaves);
+  const Dest dst = uniform_dest(a, u, D);
+  mfma_segment<E, KVF, D, NT>(a, lds + half * MfmaLds<D, NT>::kBytes, u, dst, wave - half * kWaves);
+  if constexpr (NT == 1) {
+    if (!dst.final && a.arrivals != nullptr) {
+      arrive_and_merge<E>(unit_counter(a, u), uniform_job<E>(a, u, D, active_splits(a, u)), D, wave - half * kWaves,
+                          s_last + half);
+    }
+  }
 }
 
 // ------------------------------------------------------- balanced schedule
@@ -796,7 +934,17 @@ template <typename E, typename KVF, int D, int NT>
 __global__ void __launch_bounds__(kThreads, (mfma_waves_per_eu<D, NT>()))
     decode_mfma_balanced_kernel(const DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[MfmaLds<D, NT>::kBytes];
+  __shared__ int s_last[1];
   const int hp = a.num_kv_heads * a.head_groups;  // units per sequence
+  if (a.arrivals != nullptr) {
+    // No merge kernel follows: empty sequences get their zeros here.
+    for (int b = blockIdx.x; b < a.batch; b += gridDim.x) {
+      if (seq_pages_uniform(a, b) == 0) {
+        typename E::S* out = static_cast<typename E::S*>(a.out) + static_cast<int64_t>(b) * a.num_q_heads * D;
+        for (int i = threadIdx.x; i < a.num_q_heads * D; i += blockDim.x) out[i] = E::from_f32(0.0f);
+      }
+    }
+  }
   const Start st = schedule_start(a, hp, blockIdx.x);
   int64_t pos = st.pos;
   const int64_t end = min(pos + st.per, st.total);
@@ -835,6 +983,25 @@ __global__ void __launch_bounds__(kThreads, (mfma_waves_per_eu<D, NT>()))
 
     __syncthreads();  // the previous segment's wave 0 may still read LDS
     mfma_segment<E, KVF, D, NT>(a, lds, u, dst, wave_id());
+    if (NT == 1 && !dst.final && a.arrivals != nullptr) {
+      // The unit's segments are workgroups w0 .. w1 (slots w + unit).
+      const int64_t w0 = unit_base / st.per;
+      const int64_t w1 = (unit_base + n - 1) / st.per;
+      const int64_t slot0 = w0 + static_cast<int64_t>(b) * hp + r;
+      const int h0 = u.hg * a.heads_per_wg;
+      MergeJob job;
+      job.lse = a.lse_part + slot0 * a.heads_per_wg;
+      job.lse_head_stride = 1;
+      job.l_stride = a.heads_per_wg;
+      job.o = a.o_part + slot0 * a.heads_per_wg * D;
+      job.o_head_stride = D;
+      job.o_stride = static_cast<int64_t>(a.heads_per_wg) * D;
+      job.n = static_cast<int>(w1 - w0) + 1;
+      job.heads = min(a.heads_per_wg, a.group - h0);
+      job.out = static_cast<typename E::S*>(a.out) +
+                (static_cast<int64_t>(u.b) * a.num_q_heads + u.kvh * a.group + h0) * D;
+      arrive_and_merge<E>(a.arrivals + static_cast<int64_t>(b) * hp + r, job, D, wave_id(), s_last);
+    }
 
     pos = unit_base + page1;
     if (r == hp - 1 && page1 == n) {  // this sequence's units are done: next non-empty one
@@ -1043,27 +1210,41 @@ __global__ void __launch_bounds__(kThreads) decode_valu_kernel(const DecodeArgs 
 // partial rows l / C, l / C + R, ... (R = 64 / C rows per wave-wide load),
 // up to kG rows per lane per round, each with its lse. The first round's loads go
 // out before the lse loads of the max and the sum, so for up to kG * R
-// partials (32 at head_dim 128) the merge waits for memory once. Indexes are
-// clamped (weight 0 past the end); rows are then summed across the R lane
-// groups with xor shuffles.
-template <typename E>
-__device__ __forceinline__ void merge_partials(const float* lse, int64_t l_stride, const float* op,
-                                               int64_t o_stride, int n, int head_dim, typename E::S* out);
-
+// partials (32 at head_dim 128 with kG = 16) the merge waits for memory once.
+// Indexes are clamped (weight 0 past the end); rows are then summed across the
+// R lane groups with xor shuffles. Each lane group adds its rows in increasing
+// order whatever kG is, so every kG gives the same bits.
 __device__ __forceinline__ float wave_max(float v) {
   v = row16_max(v);
   return fmaxf(fmaxf(lane_read(v, 0), lane_read(v, 16)), fmaxf(lane_read(v, 32), lane_read(v, 48)));
 }
 
-template <typename E>
+template <typename E, int kG, int POL>
 __device__ __forceinline__ void merge_partials(const float* lse, int64_t l_stride, const float* op,
                                                int64_t o_stride, int n, int head_dim, typename E::S* out) {
-  constexpr int kG = 16;
   const int lane = __lane_id();
   const int cpr = head_dim >> 2;      // 16-byte chunks per row (4 .. 64)
   const int rpl = 64 / cpr;           // rows per wave-wide load
   const int c = lane & (cpr - 1);
   const int r = lane / cpr;
+  // POL != 0: buffer loads with that cache policy (op and lse are
+  // wave-uniform, a unit's partials lie within 2 GiB of them).
+  const auto orsrc = make_rsrc(uniform_ptr(op));
+  const auto lrsrc = make_rsrc(uniform_ptr(lse));
+  auto load_o = [&](int w) -> f32x4 {
+    if constexpr (POL == 0) {
+      return *reinterpret_cast<const f32x4*>(op + w * o_stride + 4 * c);
+    } else {
+      return __builtin_bit_cast(f32x4, buffer_load16<POL>(orsrc, static_cast<uint32_t>((w * o_stride + 4 * c) * 4)));
+    }
+  };
+  auto load_lse = [&](int w) -> float {
+    if constexpr (POL == 0) {
+      return lse[w * l_stride];
+    } else {
+      return buffer_load_f32<POL>(lrsrc, static_cast<uint32_t>(w * l_stride * 4));
+    }
+  };
   f32x4 v[kG];
   float lw[kG];
   auto load_round = [&](int base) {
@@ -1073,17 +1254,17 @@ __device__ __forceinline__ void merge_partials(const float* lse, int64_t l_strid
       lw[j] = -INFINITY;
       if (base + rpl * j < n) {  // wave-uniform: some lane has a row here
         const int w = min(base + r + rpl * j, n - 1);
-        v[j] = *reinterpret_cast<const f32x4*>(op + w * o_stride + 4 * c);
-        lw[j] = lse[w * l_stride];
+        v[j] = load_o(w);
+        lw[j] = load_lse(w);
       }
     }
   };
   load_round(0);
   float mx = -INFINITY;
-  for (int w = lane; w < n; w += 64) mx = fmaxf(mx, lse[w * l_stride]);
+  for (int w = lane; w < n; w += 64) mx = fmaxf(mx, load_lse(w));
   mx = wave_max(mx);
   float den = 0.0f;
-  for (int w = lane; w < n; w += 64) den += exp2f(lse[w * l_stride] - mx);
+  for (int w = lane; w < n; w += 64) den += exp2f(load_lse(w) - mx);
   den = wave_sum(den);
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
   const int per_round = kG * rpl;
@@ -1278,6 +1459,55 @@ bool pairing_enabled() {
   if (!KL_DECODE_PAIRED) return false;
   const char* v = std::getenv("KL_DECODE_PAIRED");
   return v == nullptr || v[0] != '0';
+}
+
+// KL_DECODE_FUSED_MERGE=0 sends every split decode to the merge kernels.
+bool fused_merge_enabled() {
+  if (!KL_DECODE_FUSED_MERGE) return false;
+  const char* v = std::getenv("KL_DECODE_FUSED_MERGE");
+  return v == nullptr || v[0] != '0';
+}
+
+// The arrival-counter region of `stream` on the current device (taken on the
+// stream's first fused call and kept: a stream's kernels run one after
+// another, so its calls can share one region), or null when every region of
+// the device belongs to other streams or the counters cannot be located.
+uint32_t* arrival_region(hipStream_t stream) {
+  struct Device {
+    uint32_t* base = nullptr;
+    bool located = false;
+    hipStream_t owner[kArrivalRegions] = {};
+    int taken = 0;
+  };
+  static std::mutex mu;
+  static std::vector<Device> devices;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (static_cast<size_t>(dev) >= devices.size()) devices.resize(dev + 1);
+  Device& d = devices[dev];
+  if (!d.located) {
+    d.located = true;
+    void* p = nullptr;
+    // The device array's own name is a host-side stand-in: its device address
+    // comes from the runtime, once per device.
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_decode_arrivals)) == hipSuccess) d.base = static_cast<uint32_t*>(p);
+  }
+  if (d.base == nullptr) return nullptr;
+  for (int i = 0; i < d.taken; ++i) {
+    if (d.owner[i] == stream) return d.base + static_cast<size_t>(i) * kArrivalCounters;
+  }
+  if (d.taken == kArrivalRegions) return nullptr;
+  d.owner[d.taken] = stream;
+  return d.base + static_cast<size_t>(d.taken++) * kArrivalCounters;
+}
+
+// Arrival counters for a split decode of `units` units with up to
+// heads_per_wg heads each on the MFMA path, or null for the merge kernel.
+uint32_t* fused_merge_counters(const DecodeArgs& a, int64_t units, hipStream_t stream) {
+  if (!fused_merge_enabled() || units > kArrivalCounters || a.heads_per_wg > kFusedMergeMaxHeads) return nullptr;
+  if (a.q_fold != a.group || a.force_partial) return nullptr;  // cascade passes keep their own merge
+  return arrival_region(stream);
 }
 
 bool valu_head_dim_ok(kl_dtype dtype, int head_dim) {
@@ -1492,8 +1722,9 @@ int launch_uniform_mfma(const DecodeArgs& a, int head_dim, unsigned grid, hipStr
 }
 
 template <typename E, typename KVF>
-int launch_balanced(const DecodeArgs& a, int head_dim, hipStream_t stream) {
+int launch_balanced(DecodeArgs a, int head_dim, hipStream_t stream) {
   const unsigned grid = static_cast<unsigned>(a.grid);
+  a.arrivals = fused_merge_counters(a, static_cast<int64_t>(a.batch) * a.num_kv_heads * a.head_groups, stream);
   int st = dispatch_mfma(head_dim, a.heads_per_wg, [&](auto d, auto nt) -> int {
     constexpr int D = decltype(d)::value, NT = decltype(nt)::value;
     if constexpr (mfma_instance_exists<KVF, D>()) {
@@ -1505,7 +1736,7 @@ int launch_balanced(const DecodeArgs& a, int head_dim, hipStream_t stream) {
   });
   if (st != KL_OK) return st;
   st = check_launch("paged decode balanced kernel launch");
-  if (st != KL_OK) return st;
+  if (st != KL_OK || a.arrivals != nullptr) return st;
   decode_merge_balanced_kernel<E>
       <<<static_cast<unsigned>(static_cast<int64_t>(a.batch) * a.num_q_heads), 64, 0, stream>>>(a, head_dim);
   return check_launch("paged decode balanced merge kernel launch");
@@ -1522,6 +1753,9 @@ int launch_typed(DecodeArgs& a, int head_dim, bool mfma, hipStream_t stream) {
   }
   const int64_t wgs = static_cast<int64_t>(a.batch) * a.num_kv_heads * a.head_groups * a.num_splits;
   if (wgs > 0x7fffffffLL) return fail(KL_ERR_UNSUPPORTED, "too many workgroups");
+  if (mfma && a.num_splits > 1) {
+    a.arrivals = fused_merge_counters(a, static_cast<int64_t>(a.batch) * a.num_kv_heads * a.head_groups, stream);
+  }
   int st;
   if constexpr (!std::is_same_v<E, F32>) {
     st = mfma ? launch_uniform_mfma<E, KVF>(a, head_dim, static_cast<unsigned>(wgs), stream)
@@ -1532,7 +1766,7 @@ int launch_typed(DecodeArgs& a, int head_dim, bool mfma, hipStream_t stream) {
   if (st != KL_OK) return st;
   st = check_launch("paged decode split kernel launch");
   if (st != KL_OK) return st;
-  if (a.num_splits > 1) {
+  if (a.num_splits > 1 && a.arrivals == nullptr) {
     decode_merge_kernel<E><<<static_cast<unsigned>(static_cast<int64_t>(a.batch) * a.num_q_heads), 64, 0, stream>>>(
         a, head_dim);
     st = check_launch("paged decode merge kernel launch");
@@ -1633,6 +1867,7 @@ int decode_entry(kl_dtype dtype, bool kv8, void* out, const void* q, const void*
   a.q_heads = num_q_heads;
   a.force_partial = 0;
   a.paired = p.paired ? 1 : 0;
+  a.arrivals = nullptr;
 
   const bool mfma = use_mfma && mfma_path(dtype, head_dim, page_size);
   switch (dtype) {
@@ -1848,6 +2083,7 @@ extern "C" int kl_cascade_decode_attention(kl_dtype dtype, void* out, const void
   a.page_size = page_size;
   a.grid = 0;
   a.paired = 0;
+  a.arrivals = nullptr;
   a.scale_log2 = scale * kLog2e;
   a.q_fold = a.group;
   a.q_heads = num_q_heads;

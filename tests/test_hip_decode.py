@@ -242,6 +242,27 @@ def test_config4_long_context_gqa(gpu_ops):
     assert err < 1.6e-2, err
 
 
+def test_config4_131072_context(gpu_ops):
+    """64/8/128/16 bf16, B 8, ctx 131072 (4.3 GB of cache), planner splits.
+
+    The oracle checks 2 of the 8 sequences (a bounded CPU cost); every
+    sequence is pinned by linearity in V: doubling V doubles the output bit
+    for bit (products and fp32 sums scale exactly by 2, the log-sum-exp merge
+    weights do not change, and rounding commutes with a power of two).
+    """
+    q, kv = device_decode_problem([131072] * 8, 64, 8, 128, 16, dtype=torch.bfloat16, seed=5)
+    got = run(gpu_ops, q, kv)
+    assert torch.isfinite(got).all()
+    rows = [0, 7]
+    want = ref.paged_decode_attention(
+        q[rows].cpu(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table[rows].cpu(), kv.seq_lens[rows].cpu()
+    )
+    check(got[rows], want, torch.bfloat16)
+    kv.v_cache.mul_(2)  # NaN spares stay NaN; N(0,1) values stay far from overflow
+    doubled = run(gpu_ops, q, kv)
+    assert torch.equal(doubled, got * 2), "output is not exactly linear in V"
+
+
 # ------------------------------------------- balanced schedule (planner path)
 
 

@@ -1,0 +1,171 @@
+"""Split units merged inside the decode kernel (no merge launch).
+
+On the MFMA path, a unit split over several segments (uniform splits, or a
+balanced-schedule workgroup range) with at most 8 query heads is merged by
+its last segment to finish, counted on library-owned arrival counters of a
+region that belongs to the call's stream. The merge is the merge kernels' own
+routine, so every output must be bit-identical with the fused merge switched
+off (``KL_DECODE_FUSED_MERGE=0``), and match the oracle. The counters must be
+left at zero by every call (back-to-back calls of different shapes), streams
+must not share counters (concurrent streams), and a stream beyond the
+library's 16 regions per device must fall back to the merge kernel.
+"""
+
+from __future__ import annotations
+
+import os
+
+import pytest
+import torch
+
+from kernel_lab.kv_cache import device_decode_problem, quantize_fp8, random_decode_problem
+from oracle import reference as ref
+from tests.conftest import tolerance
+
+pytestmark = pytest.mark.gpu
+
+
+def _decode(ops, q, kv, out=None, **kw):
+    return ops.paged_decode_attention(q, kv.k_cache, kv.v_cache, kv.block_table, kv.seq_lens, out=out, **kw)
+
+
+def _unfused(fn):
+    old = os.environ.get("KL_DECODE_FUSED_MERGE")
+    os.environ["KL_DECODE_FUSED_MERGE"] = "0"
+    try:
+        return fn()
+    finally:
+        if old is None:
+            del os.environ["KL_DECODE_FUSED_MERGE"]
+        else:
+            os.environ["KL_DECODE_FUSED_MERGE"] = old
+
+
+def _lens(batch: int, hi: int, seed: int) -> list[int]:
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(1, hi + 1, (batch,), generator=g).tolist()
+
+
+CASES = [
+    # (lens, hq, hkv, head_dim, dtype, num_splits, empty rows); None = planner
+    ([512], 32, 8, 128, torch.float16, None, []),  # balanced, B=1
+    ([4096] * 8, 32, 8, 128, torch.float16, None, []),  # balanced, units split 4 ways
+    ([65536] + [1024] * 15, 32, 8, 128, torch.float16, None, []),  # skewed, balanced
+    ("r24", 64, 8, 128, torch.bfloat16, None, [3, 17]),  # G=8, empty sequences
+    ("r64", 32, 8, 128, torch.float16, -1, [0, 63]),  # balanced on request, full batch
+    ([900] * 8, 32, 8, 128, torch.float16, 4, []),  # uniform splits
+    ([1, 15, 16, 17, 33, 70, 300, 1025], 16, 4, 64, torch.bfloat16, 16, [2]),  # splits past short sequences
+    ("r16", 8, 8, 32, torch.float16, 5, []),  # G=1, head_dim 32
+    ([2000] * 64, 32, 8, 128, torch.float16, 2, [5]),  # paired workgroups with splits
+]
+
+
+def _case_lens(spec):
+    if isinstance(spec, str):
+        n = int(spec[1:])
+        return _lens(n, 3000, seed=n)
+    return list(spec)
+
+
+@pytest.mark.parametrize(("spec", "hq", "hkv", "head_dim", "dtype", "num_splits", "empty"), CASES)
+def test_fused_merge_is_bit_identical(gpu_ops, spec, hq, hkv, head_dim, dtype, num_splits, empty):
+    lens = _case_lens(spec)
+    q, kv = device_decode_problem(lens, hq, hkv, head_dim, 16, dtype=dtype, seed=len(lens) + hq)
+    if empty:
+        kv.seq_lens[empty] = 0
+    kw = {} if num_splits is None else {"num_splits": num_splits}
+    fused = _decode(gpu_ops, q, kv, **kw).cpu()
+    merged = _unfused(lambda: _decode(gpu_ops, q, kv, **kw)).cpu()
+    assert torch.isfinite(fused).all(), "non-finite output: a poisoned page or tail leaked in"
+    assert torch.equal(fused, merged), "fused merge differs from the merge kernel"
+    for b in empty:
+        assert not fused[b].any(), "an empty sequence must give zeros"
+    rows = [b for b in range(len(lens)) if b not in empty][:6]
+    want = ref.paged_decode_attention(
+        q[rows].cpu(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table[rows].cpu(), kv.seq_lens[rows].cpu()
+    )
+    torch.testing.assert_close(fused[rows], want, **tolerance(dtype))
+
+
+def test_fused_merge_fp8_cache(gpu_ops):
+    q, kv, _, _ = random_decode_problem([3000, 20, 700, 1], 32, 8, 128, 16, dtype=torch.bfloat16,
+                                        device="cuda", poison=float("nan"))
+    kv8, ks, vs = quantize_fp8(kv)
+    run = lambda: gpu_ops.paged_decode_attention(q, kv8.k_cache, kv8.v_cache, kv.block_table, kv.seq_lens,
+                                                 k_scale=ks, v_scale=vs)
+    fused = run().cpu()
+    assert torch.equal(fused, _unfused(run).cpu())
+    want = ref.paged_decode_attention_fp8(
+        q.cpu(), kv8.k_cache.cpu(), kv8.v_cache.cpu(), kv.block_table.cpu(), kv.seq_lens.cpu(), ks.cpu(), vs.cpu()
+    )
+    torch.testing.assert_close(fused, want, **tolerance(torch.bfloat16))
+
+
+def test_counters_are_left_at_zero(gpu_ops):
+    """Back-to-back calls whose units overlap in the counter array, with
+    different segment counts: a counter left nonzero by one call would make a
+    later call merge early or never."""
+    problems = []
+    for i, (lens, splits) in enumerate([([700] * 8, 3), ([4096] * 2, None), ([300] * 16, 7), ([9000], None)]):
+        q, kv = device_decode_problem(lens, 32, 8, 128, 16, dtype=torch.float16, seed=40 + i)
+        kw = {} if splits is None else {"num_splits": splits}
+        want = _unfused(lambda q=q, kv=kv, kw=kw: _decode(gpu_ops, q, kv, **kw)).clone()
+        problems.append((q, kv, kw, want))
+    for _ in range(5):
+        for q, kv, kw, want in problems:
+            assert torch.equal(_decode(gpu_ops, q, kv, **kw), want)
+    torch.cuda.synchronize()
+
+
+def test_concurrent_streams(gpu_ops):
+    """Calls in flight on several streams at once take separate counter
+    regions; each stream's results equal the unfused ones."""
+    jobs = []
+    for i in range(4):
+        q, kv = device_decode_problem([2500] * 6, 32, 8, 128, 16, dtype=torch.float16, seed=60 + i)
+        want = _unfused(lambda q=q, kv=kv: _decode(gpu_ops, q, kv)).clone()
+        jobs.append((torch.cuda.Stream(), q, kv, torch.empty_like(q), want))
+    torch.cuda.synchronize()
+    for _ in range(3):
+        for stream, q, kv, out, _ in jobs:
+            stream.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(stream):
+                for _ in range(4):
+                    _decode(gpu_ops, q, kv, out=out)
+        torch.cuda.synchronize()
+        for _, _, _, out, want in jobs:
+            assert torch.equal(out, want)
+
+
+def test_streams_beyond_the_regions_fall_back(gpu_ops):
+    """More streams than counter regions: the extra streams use the merge
+    kernel and still give the same bits."""
+    q, kv = device_decode_problem([1800] * 4, 32, 8, 128, 16, dtype=torch.float16, seed=80)
+    want = _unfused(lambda: _decode(gpu_ops, q, kv)).clone()
+    outs = []
+    for _ in range(24):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        out = torch.empty_like(q)
+        with torch.cuda.stream(s):
+            _decode(gpu_ops, q, kv, out=out)
+        outs.append(out)
+    torch.cuda.synchronize()
+    for out in outs:
+        assert torch.equal(out, want)
+
+
+@pytest.mark.parametrize(("lens", "splits"), [([4096] * 8, None), ([900] * 16, 6), ([30000, 40, 500], None)])
+def test_fresh_partials_every_call(gpu_ops, lens, splits):
+    """New queries on every call, so every call's partials differ from the
+    last call's at the same workspace addresses: a merge that read a partial
+    before its writer's stores were visible would differ from the merge
+    kernel's result."""
+    q, kv = device_decode_problem(lens, 32, 8, 128, 16, dtype=torch.float16, seed=90)
+    kw = {} if splits is None else {"num_splits": splits}
+    gen = torch.Generator(device="cuda").manual_seed(91)
+    for i in range(30):
+        q.normal_(generator=gen)
+        fused = _decode(gpu_ops, q, kv, **kw)
+        merged = _unfused(lambda: _decode(gpu_ops, q, kv, **kw))
+        assert torch.equal(fused, merged), f"call {i}: fused merge differs from the merge kernel"
