@@ -89,6 +89,9 @@ namespace {
 #ifndef KL_DECODE_PAIRED
 #define KL_DECODE_PAIRED 1  // two adjacent KV heads per 8-wave workgroup where the pairs fill the device
 #endif
+#ifndef KL_DECODE_BALANCED_WAVES
+#define KL_DECODE_BALANCED_WAVES 4  // waves of a balanced-schedule workgroup (head_dim <= 128)
+#endif
 #ifndef KL_DECODE_FUSED_MERGE
 #define KL_DECODE_FUSED_MERGE 1  // the last segment of a split unit merges it (no merge kernel)
 #endif
@@ -250,7 +253,7 @@ struct Mfma<BF16> {
 
 // LDS bytes the MFMA kernel needs: the per-wave K and V staging tiles during
 // the main loop, reused for the cross-wave merge afterwards.
-template <int D, int NT>
+template <int D, int NT, int W = kWaves>
 struct MfmaLds {
   // Row strides of a staged token. K: 8 elements (16 B) of pad put the 16
   // rows one ds_read_b128 touches on distinct 16-byte bank groups. V: 16
@@ -259,9 +262,9 @@ struct MfmaLds {
   static constexpr int kKRow = D + 8;
   static constexpr int kVRow = D + 16;
   static constexpr int kWaveStage = kBlock * (kKRow + kVRow);  // elements per wave
-  static constexpr int kStageBytes = kWaves * kWaveStage * 2;
-  static constexpr int kAccBytes = (kWaves - 1) * NT * (D / 16) * 4 * 64 * 4;
-  static constexpr int kMlBytes = kWaves * NT * 16 * 2 * 4;
+  static constexpr int kStageBytes = W * kWaveStage * 2;
+  static constexpr int kAccBytes = (W - 1) * NT * (D / 16) * 4 * 64 * 4;
+  static constexpr int kMlBytes = W * NT * 16 * 2 * 4;
   static constexpr int kBytes =
       kStageBytes > kAccBytes + kMlBytes ? kStageBytes : kAccBytes + kMlBytes;
 };
@@ -315,7 +318,7 @@ struct Dest {
 // formats share every instruction. An FP8 cache's per-head scales are folded
 // into the score scale (K) and the epilogue (V): q.(s_k k) = s_k (q.k) and
 // sum p (s_v v) = s_v sum p v.
-template <typename E, typename KVF, int D, int NT>
+template <typename E, typename KVF, int D, int NT, int W = kWaves>
 __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, const Unit& u, const Dest& dst,
                                              const int wave) {
   using S = typename E::S;
@@ -330,8 +333,8 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
   constexpr int TPL = 64 / LPT;        // tokens per load instruction
   constexpr int NL = kBlock / TPL;     // 16-byte loads per lane per block, each of K and V
   static_assert(TPL <= kBlock && kBlock % TPL == 0, "a load must stay inside its 16-token block");
-  constexpr int KROW = MfmaLds<D, NT>::kKRow;
-  constexpr int VROW = MfmaLds<D, NT>::kVRow;
+  constexpr int KROW = MfmaLds<D, NT, W>::kKRow;
+  constexpr int VROW = MfmaLds<D, NT, W>::kVRow;
   constexpr int NS = mfma_stages<D>();
 
   const int lane = __lane_id();
@@ -380,9 +383,9 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
   const int bpp = a.page_size / kBlock;  // blocks per page
   const int blk_begin = u.page_begin * bpp;
   const int blk_end = min(u.page_end * bpp, (u.seq_len + kBlock - 1) / kBlock);
-  // This wave's blocks: blk_begin + wave + kWaves * i, i < nblk.
+  // This wave's blocks: blk_begin + wave + W * i, i < nblk.
   const int first = blk_begin + wave;
-  const int nblk = first < blk_end ? (blk_end - first + kWaves - 1) / kWaves : 0;
+  const int nblk = first < blk_end ? (blk_end - first + W - 1) / W : 0;
 
   // Per-lane byte offsets inside a block (token row x head dims), for buffer
   // loads off a per-block wave-uniform base. Load c covers tokens
@@ -400,7 +403,7 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
   // markedly faster than the MFMA operand layout, and are re-laid out through
   // this wave's LDS tiles: K rows are read back as the A operand (lane = token,
   // 8 dims), V through the transposing read.
-  S* kstage = reinterpret_cast<S*>(lds) + wave * MfmaLds<D, NT>::kWaveStage;
+  S* kstage = reinterpret_cast<S*>(lds) + wave * MfmaLds<D, NT, W>::kWaveStage;
   S* stage = kstage + kBlock * KROW;
   const S* k_src = kstage + row * KROW + 8 * grp;
   // Source of this lane's 8-byte chunk in the transposing V^T read: token
@@ -409,7 +412,7 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
 
   // Element offset of this wave's i-th block (wave-uniform, scalar math).
   auto block_base = [&](int i) -> int64_t {
-    const int blk = first + kWaves * i;
+    const int blk = first + W * i;
     const int pidx = blk / bpp;
     return static_cast<int64_t>(bt[pidx]) * a.page_stride +
            static_cast<int64_t>((blk - pidx * bpp) * kBlock) * a.token_stride + static_cast<int64_t>(u.kvh) * D;
@@ -445,7 +448,7 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
   auto process_block = [&](int i, const u32x4 (&kf)[NL], const u32x4 (&vf)[NL], auto&& mid) {
     // Valid tokens in the block: >= 16 means all; <= 0 only for the padding
     // slots of the last pipeline round (i >= nblk).
-    const int nvalid = i < nblk ? u.seq_len - (first + kWaves * i) * kBlock : 0;
+    const int nvalid = i < nblk ? u.seq_len - (first + W * i) * kBlock : 0;
 
     // Stage K (its rows past seq_len only feed scores replaced by -inf below).
 #pragma unroll
@@ -546,7 +549,7 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
   // to leave the main loop first.
   __syncthreads();
   float* lds_acc = reinterpret_cast<float*>(lds);
-  float* lds_ml = lds_acc + (kWaves - 1) * NT * DT * 4 * 64;
+  float* lds_ml = lds_acc + (W - 1) * NT * DT * 4 * 64;
   if (lane < 16) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -571,18 +574,18 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
 
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
-    float mw[kWaves], lw[kWaves];
+    float mw[W], lw[W];
     float mmax = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < W; ++w) {
       mw[w] = lds_ml[((w * NT + t) * 16 + row) * 2 + 0];
       lw[w] = lds_ml[((w * NT + t) * 16 + row) * 2 + 1];
       mmax = fmaxf(mmax, mw[w]);
     }
-    float cw[kWaves];
+    float cw[W];
     float denom = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < W; ++w) {
       cw[w] = mw[w] == -INFINITY ? 0.0f : exp2f(mw[w] - mmax);
       denom += lw[w] * cw[w];
     }
@@ -596,7 +599,7 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
       for (int i = 0; i < 4; ++i) {
         float num = acc[t][dt][i] * cw[0];
 #pragma unroll
-        for (int w = 1; w < kWaves; ++w) {
+        for (int w = 1; w < W; ++w) {
           num += lds_acc[((((w - 1) * NT + t) * DT + dt) * 4 + i) * 64 + lane] * cw[w];
         }
         o[i] = num / denom * out_scale;
@@ -670,7 +673,7 @@ struct MergeJob {
 // stores to complete before the device-scope add makes them visible to
 // whoever sees the add. Acquire: the last arriver reads the partials with
 // device-coherent loads, issued only after the add returned.
-template <typename E>
+template <typename E, int W = kWaves>
 __device__ void arrive_and_merge(uint32_t* counter, const MergeJob& job, int head_dim, int wave, int* s_last) {
   if (wave == 0) {
     wait_vector_memory();
@@ -687,7 +690,7 @@ __device__ void arrive_and_merge(uint32_t* counter, const MergeJob& job, int hea
   if (!last) return;
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");  // no load moves above the arrival
   using S = typename E::S;
-  for (int h = wave; h < job.heads; h += kWaves) {
+  for (int h = wave; h < job.heads; h += W) {
     // 4 rows per lane per round: a unit rarely has more than 8 segments, and
     // the decode kernel's registers stay within its occupancy budget.
     merge_partials<E, 4, kCachePolicyDevice>(job.lse + h * job.lse_head_stride, job.l_stride,
@@ -886,6 +889,8 @@ __device__ __forceinline__ void list_prefix(const DecodeArgs& a, int units_per_s
 struct Start {
   int64_t total, per, pos, base;
   int b;
+  int pages;      // pages of sequence b (when b < batch)
+  int wg_empty;   // batch <= 64 only: sequence `wg` exists and has no pages
 };
 
 __device__ __forceinline__ Start schedule_start(const DecodeArgs& a, int units_per_seq, int wg) {
@@ -898,15 +903,20 @@ __device__ __forceinline__ Start schedule_start(const DecodeArgs& a, int units_p
     s.per = balanced_per(a, s.total);
     s.pos = static_cast<int64_t>(wg) * s.per;
     const uint64_t hit = __ballot(incl > s.pos);
+    s.wg_empty = wg < a.batch && __builtin_amdgcn_readlane(pl, wg & 63) == 0;
     if (hit == 0) {
       s.b = a.batch;
       s.base = s.total;
+      s.pages = 0;
     } else {
       const int j = __builtin_ctzll(hit);
       s.b = j;
       s.base = __builtin_amdgcn_readlane(incl - pl, j);
+      s.pages = __builtin_amdgcn_readlane(pl, j) / units_per_seq;
     }
   } else {
+    s.wg_empty = 0;
+    s.pages = 0;
     s.total = list_total(a, units_per_seq);
     s.per = balanced_per(a, s.total);
     s.pos = static_cast<int64_t>(wg) * s.per;
@@ -921,39 +931,60 @@ __device__ __forceinline__ Start schedule_start(const DecodeArgs& a, int units_p
         const int j = __builtin_ctzll(__ballot(s.base + incl > s.pos));
         s.b = b0 + j;
         s.base += __builtin_amdgcn_readlane(incl - pl, j);
+        s.pages = __builtin_amdgcn_readlane(pl, j) / units_per_seq;
         break;
       }
       s.base += chunk;
     }
   }
   s.b = __builtin_amdgcn_readfirstlane(s.b);
+  s.pages = __builtin_amdgcn_readfirstlane(s.pages);
+  s.wg_empty = __builtin_amdgcn_readfirstlane(s.wg_empty);
   return s;
 }
 
+// Waves of a balanced-schedule workgroup (one workgroup per CU). Measured on
+// MI355X, 8 waves instead of 4 were slower at batch 1-16 (B=1 ctx 512: 15.6
+// vs 12.9 us, B=8 ctx 512: 18.0 vs 14.4 us) and equal on long contexts: these
+// launches are bound by latency chains and the cross-wave merge, not by the
+// loads in flight. head_dim 256 always takes 4 (8 waves cap a wave at 256
+// registers, below what its segment needs).
+template <int D>
+constexpr int balanced_waves() {
+  return D <= 128 ? KL_DECODE_BALANCED_WAVES : kWaves;
+}
+
 template <typename E, typename KVF, int D, int NT>
-__global__ void __launch_bounds__(kThreads, (mfma_waves_per_eu<D, NT>()))
+__global__ void __launch_bounds__(balanced_waves<D>() * 64, (mfma_waves_per_eu<D, NT>()))
     decode_mfma_balanced_kernel(const DecodeArgs a) {
-  __shared__ __attribute__((aligned(16))) char lds[MfmaLds<D, NT>::kBytes];
+  constexpr int W = balanced_waves<D>();
+  __shared__ __attribute__((aligned(16))) char lds[MfmaLds<D, NT, W>::kBytes];
   __shared__ int s_last[1];
   const int hp = a.num_kv_heads * a.head_groups;  // units per sequence
+  const Start st = schedule_start(a, hp, blockIdx.x);
   if (a.arrivals != nullptr) {
-    // No merge kernel follows: empty sequences get their zeros here.
-    for (int b = blockIdx.x; b < a.batch; b += gridDim.x) {
-      if (seq_pages_uniform(a, b) == 0) {
-        typename E::S* out = static_cast<typename E::S*>(a.out) + static_cast<int64_t>(b) * a.num_q_heads * D;
-        for (int i = threadIdx.x; i < a.num_q_heads * D; i += blockDim.x) out[i] = E::from_f32(0.0f);
+    // No merge kernel follows: empty sequences get their zeros here, sequence
+    // b from workgroup b % grid (a batch of up to 64 from the schedule's scan).
+    auto zero = [&](int b) {
+      typename E::S* out = static_cast<typename E::S*>(a.out) + static_cast<int64_t>(b) * a.num_q_heads * D;
+      for (int i = threadIdx.x; i < a.num_q_heads * D; i += blockDim.x) out[i] = E::from_f32(0.0f);
+    };
+    if (a.batch <= 64) {
+      if (st.wg_empty) zero(blockIdx.x);
+    } else {
+      for (int b = blockIdx.x; b < a.batch; b += gridDim.x) {
+        if (seq_pages_uniform(a, b) == 0) zero(b);
       }
     }
   }
-  const Start st = schedule_start(a, hp, blockIdx.x);
   int64_t pos = st.pos;
   const int64_t end = min(pos + st.per, st.total);
   int b = st.b;
   int64_t base = st.base;
+  int n = st.pages;  // pages of sequence b
 
   while (pos < end && b < a.batch) {
     // b is pages-bearing: the start and the advance below skip empty sequences.
-    const int n = seq_pages_uniform(a, b);
     const int r = static_cast<int>((pos - base) / n);
     const int page0 = static_cast<int>(pos - base - static_cast<int64_t>(r) * n);
     const int64_t unit_base = base + static_cast<int64_t>(r) * n;
@@ -982,7 +1013,7 @@ __global__ void __launch_bounds__(kThreads, (mfma_waves_per_eu<D, NT>()))
     dst.lse_head_stride = 1;
 
     __syncthreads();  // the previous segment's wave 0 may still read LDS
-    mfma_segment<E, KVF, D, NT>(a, lds, u, dst, wave_id());
+    mfma_segment<E, KVF, D, NT, W>(a, lds, u, dst, wave_id());
     if (NT == 1 && !dst.final && a.arrivals != nullptr) {
       // The unit's segments are workgroups w0 .. w1 (slots w + unit).
       const int64_t w0 = unit_base / st.per;
@@ -1000,7 +1031,7 @@ __global__ void __launch_bounds__(kThreads, (mfma_waves_per_eu<D, NT>()))
       job.heads = min(a.heads_per_wg, a.group - h0);
       job.out = static_cast<typename E::S*>(a.out) +
                 (static_cast<int64_t>(u.b) * a.num_q_heads + u.kvh * a.group + h0) * D;
-      arrive_and_merge<E>(a.arrivals + static_cast<int64_t>(b) * hp + r, job, D, wave_id(), s_last);
+      arrive_and_merge<E, W>(a.arrivals + static_cast<int64_t>(b) * hp + r, job, D, wave_id(), s_last);
     }
 
     pos = unit_base + page1;
@@ -1008,7 +1039,8 @@ __global__ void __launch_bounds__(kThreads, (mfma_waves_per_eu<D, NT>()))
       base += static_cast<int64_t>(n) * hp;
       do {
         b = __builtin_amdgcn_readfirstlane(b + 1);
-      } while (b < a.batch && seq_pages_uniform(a, b) == 0);
+        n = b < a.batch ? seq_pages_uniform(a, b) : 0;
+      } while (b < a.batch && n == 0);
     }
   }
 }
@@ -1728,7 +1760,7 @@ int launch_balanced(DecodeArgs a, int head_dim, hipStream_t stream) {
   int st = dispatch_mfma(head_dim, a.heads_per_wg, [&](auto d, auto nt) -> int {
     constexpr int D = decltype(d)::value, NT = decltype(nt)::value;
     if constexpr (mfma_instance_exists<KVF, D>()) {
-      decode_mfma_balanced_kernel<E, KVF, D, NT><<<grid, kThreads, 0, stream>>>(a);
+      decode_mfma_balanced_kernel<E, KVF, D, NT><<<grid, balanced_waves<D>() * 64, 0, stream>>>(a);
       return KL_OK;
     } else {
       return fail(KL_ERR_UNSUPPORTED, "an FP8 cache needs head_dim 64, 128 or 256");
