@@ -644,13 +644,31 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
 // merge kernel.
 constexpr int kArrivalRegions = 16;      // streams served per device
 constexpr int kArrivalCounters = 8192;   // units per region
-constexpr int kFusedMergeMaxHeads = 8;   // query heads of a unit, merged one per wave
+// Query heads of a fused unit (one head tile, at most two heads per wave).
+// Measured on MI355X for MQA units (32 heads, two head tiles): the last
+// arriver's 8-heads-per-wave merge made the ragged 64-sequence batch slower
+// than the merge kernel (52.4 vs 49.8 us), and the merge code alone slowed
+// the two-tile kernel's main loop (46 -> 50 us), so those keep the merge kernel.
+constexpr int kFusedMergeMaxHeads = 8;
 
 __device__ uint32_t g_decode_arrivals[kArrivalRegions * kArrivalCounters];
 
 template <typename E, int kG = 16, int POL = 0>
 __device__ __forceinline__ void merge_partials(const float* lse, int64_t l_stride, const float* op,
                                                int64_t o_stride, int n, int head_dim, typename E::S* out);
+
+// One head's merge inputs, loaded ahead of its reduction (head_merge_load).
+template <int kG>
+struct HeadMerge {
+  f32x4 v[kG];
+  float lw[kG];
+  float ll;  // lse of row `lane`, -inf past n
+};
+template <int kG, int POL>
+__device__ __forceinline__ void head_merge_load(HeadMerge<kG>& m, const float* lse, int64_t l_stride, const float* op,
+                                                int64_t o_stride, int n, int head_dim);
+template <typename E, int kG>
+__device__ __forceinline__ void head_merge_finish(const HeadMerge<kG>& m, int n, int head_dim, typename E::S* out);
 
 // The partials of one unit: head hl's n partials (lse at lse + hl *
 // lse_head_stride + w * l_stride, rows at o + hl * o_head_stride + w *
@@ -690,12 +708,33 @@ __device__ void arrive_and_merge(uint32_t* counter, const MergeJob& job, int hea
   if (!last) return;
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");  // no load moves above the arrival
   using S = typename E::S;
-  for (int h = wave; h < job.heads; h += W) {
-    // 4 rows per lane per round: a unit rarely has more than 8 segments, and
-    // the decode kernel's registers stay within its occupancy budget.
-    merge_partials<E, 4, kCachePolicyDevice>(job.lse + h * job.lse_head_stride, job.l_stride,
-                                             job.o + h * job.o_head_stride, job.o_stride, job.n, head_dim,
-                                             static_cast<S*>(job.out) + static_cast<int64_t>(h) * head_dim);
+  S* out = static_cast<S*>(job.out);
+  constexpr int kG = 4;  // rows per lane: one round holds kG * 256 / head_dim partials
+  if (job.n <= 64 && job.n <= kG * (256 / head_dim)) {
+    // Heads wave, wave + W, ...: the next head's loads are in flight while
+    // this one is reduced, so a wave with several heads (a 32-head MQA unit)
+    // waits for memory about once.
+    HeadMerge<kG> cur, nxt;
+    int h = wave;
+    if (h < job.heads) {
+      head_merge_load<kG, kCachePolicyDevice>(cur, job.lse + h * job.lse_head_stride, job.l_stride,
+                                              job.o + h * job.o_head_stride, job.o_stride, job.n, head_dim);
+    }
+    for (; h < job.heads; h += W) {
+      const int hn = h + W;
+      if (hn < job.heads) {
+        head_merge_load<kG, kCachePolicyDevice>(nxt, job.lse + hn * job.lse_head_stride, job.l_stride,
+                                                job.o + hn * job.o_head_stride, job.o_stride, job.n, head_dim);
+      }
+      head_merge_finish<E, kG>(cur, job.n, head_dim, out + static_cast<int64_t>(h) * head_dim);
+      cur = nxt;
+    }
+  } else {
+    for (int h = wave; h < job.heads; h += W) {
+      merge_partials<E, 4, kCachePolicyDevice>(job.lse + h * job.lse_head_stride, job.l_stride,
+                                               job.o + h * job.o_head_stride, job.o_stride, job.n, head_dim,
+                                               out + static_cast<int64_t>(h) * head_dim);
+    }
   }
 }
 
@@ -759,7 +798,7 @@ __global__ void __launch_bounds__(kThreads, (mfma_waves_per_eu<D, NT>())) decode
   }
   const Dest dst = uniform_dest(a, u, D);
   mfma_segment<E, KVF, D, NT>(a, lds, u, dst, wave_id());
-  if constexpr (NT == 1) {  // the fused merge takes units of at most kFusedMergeMaxHeads heads
+  if constexpr (NT == 1) {  // see kFusedMergeMaxHeads
     if (!dst.final && a.arrivals != nullptr) {
       arrive_and_merge<E>(unit_counter(a, u), uniform_job<E>(a, u, D, active_splits(a, u)), D, wave_id(), s_last);
     }
@@ -798,7 +837,7 @@ __global__ void __launch_bounds__(2 * kThreads, (mfma_waves_per_eu<D, NT>()))
   }
   const Dest dst = uniform_dest(a, u, D);
   mfma_segment<E, KVF, D, NT>(a, lds + half * MfmaLds<D, NT>::kBytes, u, dst, wave - half * kWaves);
-  if constexpr (NT == 1) {
+  if constexpr (NT == 1) {  // see kFusedMergeMaxHeads
     if (!dst.final && a.arrivals != nullptr) {
       arrive_and_merge<E>(unit_counter(a, u), uniform_job<E>(a, u, D, active_splits(a, u)), D, wave - half * kWaves,
                           s_last + half);
@@ -1014,7 +1053,7 @@ __global__ void __launch_bounds__(balanced_waves<D>() * 64, (mfma_waves_per_eu<D
 
     __syncthreads();  // the previous segment's wave 0 may still read LDS
     mfma_segment<E, KVF, D, NT, W>(a, lds, u, dst, wave_id());
-    if (NT == 1 && !dst.final && a.arrivals != nullptr) {
+    if (NT == 1 && !dst.final && a.arrivals != nullptr) {  // see kFusedMergeMaxHeads
       // The unit's segments are workgroups w0 .. w1 (slots w + unit).
       const int64_t w0 = unit_base / st.per;
       const int64_t w1 = (unit_base + n - 1) / st.per;
@@ -1307,6 +1346,60 @@ __device__ __forceinline__ void merge_partials(const float* lse, int64_t l_strid
       const float wt = base + r + rpl * j < n ? exp2f(lw[j] - mx) : 0.0f;
       acc += wt * v[j];
     }
+  }
+  for (int off = cpr; off < 64; off <<= 1) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc[k] += __shfl_xor(acc[k], off, 64);
+  }
+  if (r == 0) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) out[4 * c + k] = E::from_f32(acc[k] / den);
+  }
+}
+
+// merge_partials split into a load phase and a finish phase, for merges whose
+// rows all fit one round (n <= kG * 256 / head_dim) and n <= 64, so a wave can
+// issue the next head's loads before it finishes this one. The arithmetic is
+// merge_partials' own: with n <= 64, its max and sum loops give lane l the lse
+// of row l (or -inf / 0 past n), which `ll` holds here; rows past n weigh 0.
+// The results are therefore bit-identical to merge_partials.
+template <int kG, int POL>
+__device__ __forceinline__ void head_merge_load(HeadMerge<kG>& m, const float* lse, int64_t l_stride, const float* op,
+                                                int64_t o_stride, int n, int head_dim) {
+  const int lane = __lane_id();
+  const int cpr = head_dim >> 2;
+  const int rpl = 64 / cpr;
+  const int c = lane & (cpr - 1);
+  const int r = lane / cpr;
+  const auto orsrc = make_rsrc(uniform_ptr(op));
+  const auto lrsrc = make_rsrc(uniform_ptr(lse));
+#pragma unroll
+  for (int j = 0; j < kG; ++j) {
+    m.v[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    m.lw[j] = -INFINITY;
+    if (rpl * j < n) {
+      const int w = min(r + rpl * j, n - 1);
+      m.v[j] = __builtin_bit_cast(f32x4, buffer_load16<POL>(orsrc, static_cast<uint32_t>((w * o_stride + 4 * c) * 4)));
+      m.lw[j] = buffer_load_f32<POL>(lrsrc, static_cast<uint32_t>(w * l_stride * 4));
+    }
+  }
+  m.ll = lane < n ? buffer_load_f32<POL>(lrsrc, static_cast<uint32_t>(lane * l_stride * 4)) : -INFINITY;
+}
+
+template <typename E, int kG>
+__device__ __forceinline__ void head_merge_finish(const HeadMerge<kG>& m, int n, int head_dim, typename E::S* out) {
+  const int lane = __lane_id();
+  const int cpr = head_dim >> 2;
+  const int rpl = 64 / cpr;
+  const int c = lane & (cpr - 1);
+  const int r = lane / cpr;
+  const float mx = wave_max(m.ll);
+  const float den = wave_sum(lane < n ? exp2f(m.ll - mx) : 0.0f);
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int j = 0; j < kG; ++j) {
+    const float wt = r + rpl * j < n ? exp2f(m.lw[j] - mx) : 0.0f;
+    acc += wt * m.v[j];
   }
   for (int off = cpr; off < 64; off <<= 1) {
 #pragma unroll

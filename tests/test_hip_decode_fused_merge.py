@@ -1,8 +1,9 @@
 """Split units merged inside the decode kernel (no merge launch).
 
 On the MFMA path, a unit split over several segments (uniform splits, or a
-balanced-schedule workgroup range) with at most 8 query heads is merged by
-its last segment to finish, counted on library-owned arrival counters of a
+balanced-schedule workgroup range) with one head tile of at most 8 query
+heads is merged by its last segment to finish (MQA and other two-tile units
+keep the merge kernel, and are checked here too), counted on library-owned arrival counters of a
 region that belongs to the call's stream. The merge is the merge kernels' own
 routine, so every output must be bit-identical with the fused merge switched
 off (``KL_DECODE_FUSED_MERGE=0``), and match the oracle. The counters must be
@@ -57,13 +58,16 @@ CASES = [
     ([1, 15, 16, 17, 33, 70, 300, 1025], 16, 4, 64, torch.bfloat16, 16, [2]),  # splits past short sequences
     ("r16", 8, 8, 32, torch.float16, 5, []),  # G=1, head_dim 32
     ([2000] * 64, 32, 8, 128, torch.float16, 2, [5]),  # paired workgroups with splits
+    ("m64", 32, 1, 128, torch.bfloat16, None, [9]),  # MQA: 32-head units (merge kernel), balanced
+    ([6000, 30, 2500, 800], 32, 1, 64, torch.float16, 7, []),  # MQA, uniform splits, head_dim 64
+    ([3000] * 4, 96, 4, 128, torch.float16, None, []),  # 24 heads per unit (two head tiles)
 ]
 
 
 def _case_lens(spec):
     if isinstance(spec, str):
         n = int(spec[1:])
-        return _lens(n, 3000, seed=n)
+        return _lens(n, 8192 if spec[0] == "m" else 3000, seed=n)
     return list(spec)
 
 
