@@ -928,34 +928,74 @@ __device__ __forceinline__ void list_prefix(const DecodeArgs& a, int units_per_s
 struct Start {
   int64_t total, per, pos, base;
   int b;
-  int pages;      // pages of sequence b (when b < batch)
-  int wg_empty;   // batch <= 64 only: sequence `wg` exists and has no pages
+  int pages;     // pages of sequence b (when b < batch)
+  int len;       // its length, clamped to max_pages * page_size
+  int wg_empty;  // batch <= 64 * kScanChunks only: sequence `wg` exists and has no pages
 };
+
+// Batches of up to 64 * kScanChunks sequences are scanned with all their
+// seq_lens loads in flight at once: one memory round trip at the start.
+constexpr int kScanChunks = 4;
+
+__device__ __forceinline__ int clamped_len(const DecodeArgs& a, int raw) {
+  const int64_t cap = static_cast<int64_t>(a.max_pages) * a.page_size;
+  return static_cast<int>(raw < cap ? raw : cap);
+}
+
+__device__ __forceinline__ int pages_of(const DecodeArgs& a, int len) {
+  return len > 0 ? (len + a.page_size - 1) / a.page_size : 0;
+}
 
 __device__ __forceinline__ Start schedule_start(const DecodeArgs& a, int units_per_seq, int wg) {
   const int lane = __lane_id();
   Start s;
-  if (a.batch <= 64) {
-    const int pl = lane < a.batch ? seq_pages(a, lane) * units_per_seq : 0;
-    const int incl = wave_incl_scan(pl);
-    s.total = __builtin_amdgcn_readlane(incl, 63);
+  s.wg_empty = 0;
+  s.pages = 0;
+  s.len = 0;
+  if (a.batch <= 64 * kScanChunks) {
+    int len[kScanChunks], pl[kScanChunks], incl[kScanChunks];
+    int64_t before[kScanChunks];
+    // Chunks past the batch are skipped (uniform branches): a scan is a
+    // chain of cross-lane shuffles, not free.
+#pragma unroll
+    for (int k = 0; k < kScanChunks; ++k) {
+      const int b = 64 * k + lane;
+      len[k] = 0;
+      if (64 * k < a.batch) len[k] = b < a.batch ? clamped_len(a, a.seq_lens[b]) : 0;
+    }
+    int64_t total = 0;
+#pragma unroll
+    for (int k = 0; k < kScanChunks; ++k) {
+      pl[k] = 0;
+      incl[k] = 0;
+      before[k] = total;
+      if (64 * k < a.batch) {
+        pl[k] = pages_of(a, len[k]) * units_per_seq;
+        incl[k] = wave_incl_scan(pl[k]);
+        total += __builtin_amdgcn_readlane(incl[k], 63);
+      }
+    }
+    s.total = total;
     s.per = balanced_per(a, s.total);
     s.pos = static_cast<int64_t>(wg) * s.per;
-    const uint64_t hit = __ballot(incl > s.pos);
-    s.wg_empty = wg < a.batch && __builtin_amdgcn_readlane(pl, wg & 63) == 0;
-    if (hit == 0) {
-      s.b = a.batch;
-      s.base = s.total;
-      s.pages = 0;
-    } else {
-      const int j = __builtin_ctzll(hit);
-      s.b = j;
-      s.base = __builtin_amdgcn_readlane(incl - pl, j);
-      s.pages = __builtin_amdgcn_readlane(pl, j) / units_per_seq;
+    s.b = a.batch;
+    s.base = s.total;
+    bool found = false;
+#pragma unroll
+    for (int k = 0; k < kScanChunks; ++k) {
+      if (!found && 64 * k < a.batch && before[k] + __builtin_amdgcn_readlane(incl[k], 63) > s.pos) {
+        const int j = __builtin_ctzll(__ballot(before[k] + incl[k] > s.pos));
+        s.b = 64 * k + j;
+        s.base = before[k] + __builtin_amdgcn_readlane(incl[k] - pl[k], j);
+        s.pages = __builtin_amdgcn_readlane(pl[k], j) / units_per_seq;
+        s.len = __builtin_amdgcn_readlane(len[k], j);
+        found = true;
+      }
+      if (wg >= 64 * k && wg < 64 * k + 64 && wg < a.batch) {
+        s.wg_empty = __builtin_amdgcn_readlane(pl[k], wg - 64 * k) == 0;
+      }
     }
   } else {
-    s.wg_empty = 0;
-    s.pages = 0;
     s.total = list_total(a, units_per_seq);
     s.per = balanced_per(a, s.total);
     s.pos = static_cast<int64_t>(wg) * s.per;
@@ -963,7 +1003,8 @@ __device__ __forceinline__ Start schedule_start(const DecodeArgs& a, int units_p
     s.base = 0;
     for (int b0 = 0; b0 < a.batch; b0 += 64) {
       const int b = b0 + lane;
-      const int pl = b < a.batch ? seq_pages(a, b) * units_per_seq : 0;
+      const int len = b < a.batch ? clamped_len(a, a.seq_lens[b]) : 0;
+      const int pl = pages_of(a, len) * units_per_seq;
       const int incl = wave_incl_scan(pl);
       const int chunk = __builtin_amdgcn_readlane(incl, 63);
       if (s.base + chunk > s.pos) {
@@ -971,6 +1012,7 @@ __device__ __forceinline__ Start schedule_start(const DecodeArgs& a, int units_p
         s.b = b0 + j;
         s.base += __builtin_amdgcn_readlane(incl - pl, j);
         s.pages = __builtin_amdgcn_readlane(pl, j) / units_per_seq;
+        s.len = __builtin_amdgcn_readlane(len, j);
         break;
       }
       s.base += chunk;
@@ -978,6 +1020,7 @@ __device__ __forceinline__ Start schedule_start(const DecodeArgs& a, int units_p
   }
   s.b = __builtin_amdgcn_readfirstlane(s.b);
   s.pages = __builtin_amdgcn_readfirstlane(s.pages);
+  s.len = __builtin_amdgcn_readfirstlane(s.len);
   s.wg_empty = __builtin_amdgcn_readfirstlane(s.wg_empty);
   return s;
 }
@@ -993,13 +1036,20 @@ constexpr int balanced_waves() {
   return D <= 128 ? KL_DECODE_BALANCED_WAVES : kWaves;
 }
 
-template <typename E, typename KVF, int D, int NT>
-__global__ void __launch_bounds__(balanced_waves<D>() * 64, (mfma_waves_per_eu<D, NT>()))
+// PAIR = 2 (num_kv_heads even): the work list's units are KV-head pairs (j,
+// head group); the workgroup has two halves of W waves that walk the same
+// segments, half h streaming KV head 2j + h with its own LDS (adjacent bytes
+// of every token row, as in decode_mfma_paired_kernel). Half h of segment
+// (w, list unit u) owns partial slot (w + u) * 2 + h.
+template <typename E, typename KVF, int D, int NT, int PAIR>
+__global__ void __launch_bounds__(PAIR * balanced_waves<D>() * 64, (mfma_waves_per_eu<D, NT>()))
     decode_mfma_balanced_kernel(const DecodeArgs a) {
   constexpr int W = balanced_waves<D>();
-  __shared__ __attribute__((aligned(16))) char lds[MfmaLds<D, NT, W>::kBytes];
-  __shared__ int s_last[1];
-  const int hp = a.num_kv_heads * a.head_groups;  // units per sequence
+  __shared__ __attribute__((aligned(16))) char lds[PAIR * MfmaLds<D, NT, W>::kBytes];
+  __shared__ int s_last[PAIR];
+  // A compile-time 0 with PAIR == 1, so the LDS base stays a constant.
+  const int half = PAIR == 2 ? wave_id() / W : 0;
+  const int hp = a.num_kv_heads * a.head_groups / PAIR;  // list units per sequence
   const Start st = schedule_start(a, hp, blockIdx.x);
   if (a.arrivals != nullptr) {
     // No merge kernel follows: empty sequences get their zeros here, sequence
@@ -1008,7 +1058,7 @@ __global__ void __launch_bounds__(balanced_waves<D>() * 64, (mfma_waves_per_eu<D
       typename E::S* out = static_cast<typename E::S*>(a.out) + static_cast<int64_t>(b) * a.num_q_heads * D;
       for (int i = threadIdx.x; i < a.num_q_heads * D; i += blockDim.x) out[i] = E::from_f32(0.0f);
     };
-    if (a.batch <= 64) {
+    if (a.batch <= 64 * kScanChunks) {
       if (st.wg_empty) zero(blockIdx.x);
     } else {
       for (int b = blockIdx.x; b < a.batch; b += gridDim.x) {
@@ -1020,7 +1070,8 @@ __global__ void __launch_bounds__(balanced_waves<D>() * 64, (mfma_waves_per_eu<D
   const int64_t end = min(pos + st.per, st.total);
   int b = st.b;
   int64_t base = st.base;
-  int n = st.pages;  // pages of sequence b
+  int n = st.pages;   // pages of sequence b
+  int len = st.len;   // its clamped length
 
   while (pos < end && b < a.batch) {
     // b is pages-bearing: the start and the advance below skip empty sequences.
@@ -1034,16 +1085,14 @@ __global__ void __launch_bounds__(balanced_waves<D>() * 64, (mfma_waves_per_eu<D
     // land in VGPRs and every K/V load becomes a per-lane waterfall loop.
     Unit u;
     u.b = __builtin_amdgcn_readfirstlane(b);
-    u.kvh = __builtin_amdgcn_readfirstlane(r / a.head_groups);
+    u.kvh = __builtin_amdgcn_readfirstlane((r / a.head_groups) * PAIR + half);
     u.hg = __builtin_amdgcn_readfirstlane(r % a.head_groups);
     u.split = 0;
-    const int raw = as_constant(a.seq_lens)[u.b];
-    const int64_t cap = static_cast<int64_t>(a.max_pages) * a.page_size;
-    u.seq_len = __builtin_amdgcn_readfirstlane(static_cast<int>(raw < cap ? raw : cap));
+    u.seq_len = __builtin_amdgcn_readfirstlane(len);
     u.page_begin = __builtin_amdgcn_readfirstlane(page0);
     u.page_end = __builtin_amdgcn_readfirstlane(page1);
 
-    const int64_t slot = static_cast<int64_t>(blockIdx.x) + static_cast<int64_t>(b) * hp + r;
+    const int64_t slot = (static_cast<int64_t>(blockIdx.x) + static_cast<int64_t>(b) * hp + r) * PAIR + half;
     Dest dst;
     dst.final = page0 == 0 && page1 == n;
     dst.o = a.o_part + slot * a.heads_per_wg * D;
@@ -1052,33 +1101,35 @@ __global__ void __launch_bounds__(balanced_waves<D>() * 64, (mfma_waves_per_eu<D
     dst.lse_head_stride = 1;
 
     __syncthreads();  // the previous segment's wave 0 may still read LDS
-    mfma_segment<E, KVF, D, NT, W>(a, lds, u, dst, wave_id());
+    mfma_segment<E, KVF, D, NT, W>(a, lds + half * MfmaLds<D, NT, W>::kBytes, u, dst, wave_id() - half * W);
     if (NT == 1 && !dst.final && a.arrivals != nullptr) {  // see kFusedMergeMaxHeads
-      // The unit's segments are workgroups w0 .. w1 (slots w + unit).
+      // The unit's segments are workgroups w0 .. w1 (slots (w + list unit) * PAIR + half).
       const int64_t w0 = unit_base / st.per;
       const int64_t w1 = (unit_base + n - 1) / st.per;
-      const int64_t slot0 = w0 + static_cast<int64_t>(b) * hp + r;
+      const int64_t slot0 = (w0 + static_cast<int64_t>(b) * hp + r) * PAIR + half;
       const int h0 = u.hg * a.heads_per_wg;
       MergeJob job;
       job.lse = a.lse_part + slot0 * a.heads_per_wg;
       job.lse_head_stride = 1;
-      job.l_stride = a.heads_per_wg;
+      job.l_stride = static_cast<int64_t>(PAIR) * a.heads_per_wg;
       job.o = a.o_part + slot0 * a.heads_per_wg * D;
       job.o_head_stride = D;
-      job.o_stride = static_cast<int64_t>(a.heads_per_wg) * D;
+      job.o_stride = static_cast<int64_t>(PAIR) * a.heads_per_wg * D;
       job.n = static_cast<int>(w1 - w0) + 1;
       job.heads = min(a.heads_per_wg, a.group - h0);
       job.out = static_cast<typename E::S*>(a.out) +
                 (static_cast<int64_t>(u.b) * a.num_q_heads + u.kvh * a.group + h0) * D;
-      arrive_and_merge<E, W>(a.arrivals + static_cast<int64_t>(b) * hp + r, job, D, wave_id(), s_last);
+      const int64_t unit = (static_cast<int64_t>(u.b) * a.num_kv_heads + u.kvh) * a.head_groups + u.hg;
+      arrive_and_merge<E, W>(a.arrivals + unit, job, D, wave_id() - half * W, s_last + half);
     }
 
     pos = unit_base + page1;
-    if (r == hp - 1 && page1 == n) {  // this sequence's units are done: next non-empty one
+    if (pos < end && r == hp - 1 && page1 == n) {  // more to do past this sequence: next non-empty one
       base += static_cast<int64_t>(n) * hp;
       do {
         b = __builtin_amdgcn_readfirstlane(b + 1);
-        n = b < a.batch ? seq_pages_uniform(a, b) : 0;
+        len = b < a.batch ? clamped_len(a, as_constant(a.seq_lens)[b]) : 0;
+        n = pages_of(a, len);
       } while (b < a.batch && n == 0);
     }
   }
@@ -1450,7 +1501,8 @@ __global__ void __launch_bounds__(64) decode_merge_balanced_kernel(const DecodeA
   const int hl = head % a.group;
   const int hg = hl / a.heads_per_wg;
   const int hloc = hl % a.heads_per_wg;
-  const int hp = a.num_kv_heads * a.head_groups;
+  const int pair = a.paired ? 2 : 1;  // list units are KV-head pairs (decode_mfma_balanced_kernel<..., 2>)
+  const int hp = a.num_kv_heads * a.head_groups / pair;
   int64_t total, base;  // list length; list position of sequence b's first unit
   int n;                // sequence b's pages
   list_prefix(a, hp, b, &total, &base, &n);
@@ -1461,19 +1513,21 @@ __global__ void __launch_bounds__(64) decode_merge_balanced_kernel(const DecodeA
     return;
   }
   const int64_t per = balanced_per(a, total);
-  const int r = kvh * a.head_groups + hg;
+  const int r = (kvh / pair) * a.head_groups + hg;
   const int64_t unit_base = base + static_cast<int64_t>(r) * n;
   const int64_t w0 = unit_base / per;
   const int64_t w1 = (unit_base + n - 1) / per;
   if (w0 == w1) return;
   const int64_t uidx = static_cast<int64_t>(b) * hp + r;
+  const int64_t slot0 = (w0 + uidx) * pair + kvh % pair;  // consecutive workgroups' slots are `pair` apart
   const float* lse = a.lse_part + hloc;
   const float* op = a.o_part + static_cast<int64_t>(hloc) * head_dim;
   const int64_t stride_l = a.heads_per_wg;
   const int64_t stride_o = static_cast<int64_t>(a.heads_per_wg) * head_dim;
 
   const int nw = static_cast<int>(w1 - w0) + 1;
-  merge_partials<E>(lse + (w0 + uidx) * stride_l, stride_l, op + (w0 + uidx) * stride_o, stride_o, nw, head_dim, out);
+  merge_partials<E>(lse + slot0 * stride_l, pair * stride_l, op + slot0 * stride_o, pair * stride_o, nw, head_dim,
+                    out);
 }
 
 // ---------------------------------------------------- cascade (shared prefix)
@@ -1584,6 +1638,23 @@ bool pairing_enabled() {
   if (!KL_DECODE_PAIRED) return false;
   const char* v = std::getenv("KL_DECODE_PAIRED");
   return v == nullptr || v[0] != '0';
+}
+
+// The planner's choice for fp16/bf16 batches whose units fill the device:
+// uniform splits sized from the block table's width (default), or the
+// balanced schedule with KL_DECODE_BALANCE_ALWAYS=1 in the environment (read
+// on every call; =0 forces uniform). Measured on MI355X (events, us, uniform
+// -> balanced): even batches 164.5 -> 165.0 (32/8/128 fp16 B=64 ctx 4096) up
+// to 19.5 -> 20.6 (B=32 ctx 512): the balanced start scans seq_lens before a
+// workgroup knows its first page (2.4 us against 0.85 us for the uniform
+// kernel's one scalar load); ragged lengths U[1, 8192] B=64 238 -> 217, B=32
+// 126 -> 109; one 65,536-token sequence among 63 of 2,048 tokens 1,228 -> 139.
+// Even batches keep the default; callers with uneven lengths pass
+// KL_SPLITS_BALANCED.
+bool balance_always() {
+  const char* v = std::getenv("KL_DECODE_BALANCE_ALWAYS");
+  if (v != nullptr && (v[0] == '0' || v[0] == '1')) return v[0] == '1';
+  return KL_DECODE_BALANCE_ALWAYS != 0;
 }
 
 // KL_DECODE_FUSED_MERGE=0 sends every split decode to the merge kernels.
@@ -1715,16 +1786,27 @@ int make_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads, int 
   const int cus = cu_count > 0 ? cu_count : 256;
   const int64_t units = std::max<int64_t>(1, static_cast<int64_t>(batch) * num_kv_heads * p->head_groups);
   if (num_splits == KL_SPLITS_BALANCED && (!mfma || partials)) num_splits = 0;  // uniform splits only
-  if (mfma && !partials && (num_splits == KL_SPLITS_BALANCED || (num_splits == 0 && (units < cus || KL_DECODE_BALANCE_ALWAYS)))) {
+  // The balanced schedule runs in KV-head pairs (8-wave workgroups) on
+  // batches that fill the device twice over, as uniform splits would.
+  const bool pairable = mfma && !partials && pairing_enabled() && num_kv_heads % 2 == 0 && head_dim <= 128 &&
+                        p->heads_per_wg <= 16 && units >= 2 * static_cast<int64_t>(cus);
+  const bool balance = num_splits == KL_SPLITS_BALANCED || (num_splits == 0 && (units < cus || balance_always()));
+  const bool pair_balanced = pairable && balance;
+  if (mfma && !partials && balance) {
     // Requested, or fewer units than CUs: pages balanced across sequences on the device.
-    const int64_t upper = units * pages;  // list length if every sequence were full
-    const int64_t grid = std::max<int64_t>(
-        1, std::min<int64_t>({cdiv(upper, kMinPagesPerBalancedWg),
-                              std::max<int64_t>(static_cast<int64_t>(cus) * kBalancedWgPerCu, units), 0x7fffffffLL}));
+    const int64_t lunits = pair_balanced ? units / 2 : units;  // units of the work list
+    const int64_t upper = lunits * pages;                        // list length if every sequence were full
+    // Paired: one 8-wave workgroup per CU is the register budget, so more
+    // workgroups would run in rounds, each paying the schedule's start.
+    const int64_t floor_wgs =
+        pair_balanced ? static_cast<int64_t>(cus) : std::max<int64_t>(static_cast<int64_t>(cus) * kBalancedWgPerCu, lunits);
+    const int64_t grid =
+        std::max<int64_t>(1, std::min<int64_t>({cdiv(upper, kMinPagesPerBalancedWg), floor_wgs, 0x7fffffffLL}));
     p->grid = static_cast<int>(grid);
+    p->paired = pair_balanced;
     p->num_splits = 0;
     p->pages_per_split = 0;
-    const size_t slots = static_cast<size_t>(grid) + static_cast<size_t>(units);
+    const size_t slots = (static_cast<size_t>(grid) + static_cast<size_t>(lunits)) * (pair_balanced ? 2 : 1);
     p->o_bytes = align_up(slots * p->heads_per_wg * head_dim * sizeof(float));
     p->ws_bytes = p->o_bytes + align_up(slots * p->heads_per_wg * sizeof(float));
     return ok();
@@ -1857,7 +1939,17 @@ int launch_balanced(DecodeArgs a, int head_dim, hipStream_t stream) {
   int st = dispatch_mfma(head_dim, a.heads_per_wg, [&](auto d, auto nt) -> int {
     constexpr int D = decltype(d)::value, NT = decltype(nt)::value;
     if constexpr (mfma_instance_exists<KVF, D>()) {
-      decode_mfma_balanced_kernel<E, KVF, D, NT><<<grid, balanced_waves<D>() * 64, 0, stream>>>(a);
+      if (a.paired) {
+        // One head tile and head_dim <= 128: beyond that the segment needs
+        // more than the 256 registers per lane of an 8-wave workgroup.
+        if constexpr (D <= 128 && NT == 1) {
+          decode_mfma_balanced_kernel<E, KVF, D, NT, 2><<<grid, 2 * balanced_waves<D>() * 64, 0, stream>>>(a);
+        } else {
+          return fail(KL_ERR_UNSUPPORTED, "paired balanced decode needs head_dim <= 128 and <= 16 heads per workgroup");
+        }
+      } else {
+        decode_mfma_balanced_kernel<E, KVF, D, NT, 1><<<grid, balanced_waves<D>() * 64, 0, stream>>>(a);
+      }
       return KL_OK;
     } else {
       return fail(KL_ERR_UNSUPPORTED, "an FP8 cache needs head_dim 64, 128 or 256");

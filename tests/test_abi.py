@@ -100,7 +100,7 @@ def test_planner_fills_the_device(batch, hkv, max_pages, cus, want):
 def test_planner_balances_when_units_do_not_fill_the_device(batch, hkv, max_pages, balanced):
     """fp16/bf16 with fewer (sequence, KV head) units than CUs: pages are balanced
     across sequences on the device (reported as 0 splits) with a workspace for
-    one partial per workgroup and unit."""
+    one partial per workgroup and unit; full batches take one uniform split."""
     splits, ws = ops.plan_decode(torch.float16, batch, hkv * 4, hkv, 128, 16, max_pages, 0, 256)
     if balanced:
         units = batch * hkv
@@ -110,12 +110,32 @@ def test_planner_balances_when_units_do_not_fill_the_device(batch, hkv, max_page
         assert splits == 1 and ws == 0
 
 
+@pytest.mark.parametrize(("batch", "hkv", "max_pages"), [(64, 8, 256), (32, 8, 256), (128, 8, 64), (64, 1, 512)])
+def test_balanced_planner_on_request(monkeypatch, batch, hkv, max_pages):
+    """KL_DECODE_BALANCE_ALWAYS=1 gives every fp16/bf16 batch the balanced
+    schedule (read on every call). With an even KV head count and units >=
+    2 x CUs the list runs in KV-head pairs (one 8-wave workgroup per CU), with
+    a partial slot per half."""
+    monkeypatch.setenv("KL_DECODE_BALANCE_ALWAYS", "1")
+    splits, ws = ops.plan_decode(torch.float16, batch, hkv * 4, hkv, 128, 16, max_pages, 0, 256)
+    units = batch * hkv
+    paired = hkv % 2 == 0 and units >= 512
+    lunits = units // 2 if paired else units
+    floor = 256 if paired else max(256, units)
+    grid = min(floor, -(-lunits * max_pages // 8))
+    slots = (grid + lunits) * (2 if paired else 1)
+    assert splits == 0 and ws >= slots * 4 * (128 + 1) * 4
+    monkeypatch.setenv("KL_DECODE_BALANCE_ALWAYS", "0")
+    uniform = ops.plan_decode(torch.float16, batch, hkv * 4, hkv, 128, 16, max_pages, 0, 256)[0]
+    assert uniform >= 1 if units >= 256 else uniform == 0  # fewer units than CUs: balanced regardless
+
+
 def test_requested_balanced_schedule_at_any_batch():
-    """KL_SPLITS_BALANCED (-1) picks the balanced schedule even when units fill
-    the device; the VALU path (fp32) takes the planner's uniform splits."""
+    """KL_SPLITS_BALANCED (-1) picks the balanced schedule whatever the planner
+    default; the VALU path (fp32) takes the planner's uniform splits."""
     splits, ws = ops.plan_decode(torch.float16, 64, 32, 8, 128, 16, 256, ops.BALANCED, 256)
-    units = 64 * 8
-    assert splits == 0 and ws >= (units + units) * 4 * (128 + 1) * 4
+    units = 64 * 8  # paired: 256 workgroups and 256 pair units, two slots each
+    assert splits == 0 and ws >= (256 + units // 2) * 2 * 4 * (128 + 1) * 4
     assert ops.plan_decode(torch.float32, 64, 32, 8, 128, 16, 256, ops.BALANCED, 256) == ops.plan_decode(
         torch.float32, 64, 32, 8, 128, 16, 256, 0, 256
     )

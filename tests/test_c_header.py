@@ -63,7 +63,7 @@ def test_header_compiles_as_c99_and_links(tmp_path):
     assert int(got["version"]) >= 100
     assert got["ok"] == "success"
     st, splits, ws = got["plan64"].split()
-    assert st == "0" and int(splits) >= 1
+    assert st == "0" and splits == "1" and int(ws) == 0  # one uniform split fills the device
     assert got["plan1"] == "0 0 1"  # balanced schedule for a batch of one
     assert got["planbal"] == "0 0 1"
     assert got["cascade"] == "0 1"

@@ -101,22 +101,32 @@ def test_ops_work_under_torch_compile(gpu_ops):
     torch.testing.assert_close(y.cpu(), ref_y, **tolerance(torch.float16))
 
 
-def test_balanced_request_reaches_the_planner_on_full_batches(gpu_ops):
-    """64 sequences x 8 KV heads fill the device, so the planner's own choice is
-    one uniform split (no workspace); KL_SPLITS_BALANCED (-1) still gets the
-    balanced schedule, which needs a workspace and is refused without one."""
+def test_balanced_request_reaches_the_planner_on_full_batches(gpu_ops, monkeypatch):
+    """64 sequences x 8 KV heads fill the device twice over. With
+    KL_DECODE_BALANCE_ALWAYS=1 the planner's own choice is the balanced
+    schedule in KV-head pairs (a workspace, 0 splits); by default (and with
+    =0) it is one uniform split (no workspace), and KL_SPLITS_BALANCED (-1)
+    still gets the balanced schedule, which needs a workspace and is refused
+    without one."""
     lib = _native.core()
     lens = [4000] + [100] * 63
     q, kv, _, _ = random_decode_problem(lens, 32, 8, 128, 16, dtype=torch.float16, device="cuda", poison=float("nan"))
     batch, hq, d = q.shape
     max_pages = kv.block_table.shape[1]
     code = _native.DTYPE_CODES[torch.float16]
-    sizes = {}
-    for req in (0, -1):
+
+    def plan(req):
         splits, ws = ctypes.c_int(0), ctypes.c_size_t(0)
         assert lib.kl_paged_decode_plan(code, batch, hq, 8, d, 16, max_pages, req, 0, ctypes.byref(splits), ctypes.byref(ws)) == 0
-        sizes[req] = (splits.value, ws.value)
-    assert sizes[0] == (1, 0) and sizes[-1][0] == 0 and sizes[-1][1] > 0
+        return splits.value, ws.value
+
+    assert plan(0) == (1, 0)
+    monkeypatch.setenv("KL_DECODE_BALANCE_ALWAYS", "1")
+    balanced = plan(0)
+    assert balanced[0] == 0 and balanced[1] > 0
+    monkeypatch.setenv("KL_DECODE_BALANCE_ALWAYS", "0")
+    sizes = {0: plan(0), -1: plan(-1)}
+    assert sizes[0] == (1, 0) and sizes[-1] == balanced
     out = torch.empty_like(q)
     args = [code, out.data_ptr(), q.data_ptr(), kv.k_cache.data_ptr(), kv.v_cache.data_ptr(), kv.block_table.data_ptr(),
             kv.seq_lens.data_ptr(), batch, hq, 8, d, 16, kv.block_table.stride(0), max_pages, d**-0.5, -1]

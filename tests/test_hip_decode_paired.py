@@ -1,15 +1,21 @@
 """Paired decode workgroups (two adjacent KV heads per 8-wave workgroup).
 
-With uniform splits the planner pairs the units of KV heads 2j and 2j+1 of one sequence, head
-group and split into one workgroup when the KV head count is even, head_dim
-is at most 128 and the pairs alone give each of MI355X's 256 CUs a workgroup
-(sequences x KV heads x head groups x splits >= 512). Each half runs the same
-segment code over the same blocks as the one-unit workgroup, so the output
-must be bit-identical with pairing switched off (``KL_DECODE_PAIRED=0``) and
-match the oracle. The shapes below all pair on MI355X; they cover one split
-(final outputs written by each half), requested splits with splits past the
-end of short sequences (both halves empty), empty sequences (zeros), two head
-tiles per workgroup (GQA group 24), head_dim 32 and 64, and the FP8 cache.
+Uniform splits (an explicit split count) pair the units of KV heads 2j and
+2j+1 of one sequence, head group and split into one workgroup when the KV
+head count is even, head_dim is at most 128 and the pairs alone give each of
+MI355X's 256 CUs a workgroup (sequences x KV heads x head groups x splits >=
+512). Each half runs the same segment code over the same blocks as the
+one-unit workgroup, so the output must be bit-identical with pairing switched
+off (``KL_DECODE_PAIRED=0``) and match the oracle. These shapes cover one
+split (final outputs written by each half), splits past the end of short
+sequences (both halves empty), empty sequences (zeros), two head tiles per
+workgroup (GQA group 24), head_dim 32 and 64, and the FP8 cache.
+
+The balanced schedule (the planner's choice below 256 units, and what
+``num_splits=BALANCED`` asks for) runs in KV-head pairs on batches with
+units >= 512 and one head tile: checked against the oracle and the unpaired
+balanced schedule, and, on even lengths (one pair unit per workgroup),
+bit-identical to uniform pairing.
 """
 
 from __future__ import annotations
@@ -19,7 +25,7 @@ import os
 import pytest
 import torch
 
-from kernel_lab.kv_cache import quantize_fp8, random_decode_problem
+from kernel_lab.kv_cache import device_decode_problem, quantize_fp8, random_decode_problem
 from oracle import reference as ref
 from tests.conftest import tolerance
 
@@ -69,7 +75,7 @@ def test_paired_matches_unpaired_and_oracle(gpu_ops, batch, hq, hkv, head_dim, d
     q, kv, _, _ = random_decode_problem(lens, hq, hkv, head_dim, 16, dtype=dtype, device="cuda", poison=float("nan"))
     empties = _empty_rows(batch, empty)
     kv.seq_lens[empties] = 0  # the fixture needs a token per sequence; these attend over none
-    kw = {} if num_splits is None else {"num_splits": num_splits}
+    kw = {"num_splits": 1 if num_splits is None else num_splits}  # uniform splits
     paired, single = _both(gpu_ops, q, kv, **kw)
     assert torch.isfinite(paired).all(), "non-finite output: a poisoned page or tail leaked in"
     assert torch.equal(paired, single), "paired workgroups changed the result"
@@ -87,11 +93,11 @@ def test_paired_fp8_cache_matches_unpaired(gpu_ops):
     kv8, ks, vs = quantize_fp8(kv)
     k8, v8 = kv8.k_cache, kv8.v_cache
     args = (q, k8, v8, kv.block_table, kv.seq_lens)
-    paired = gpu_ops.paged_decode_attention(*args, k_scale=ks, v_scale=vs)
+    paired = gpu_ops.paged_decode_attention(*args, k_scale=ks, v_scale=vs, num_splits=1)
     old = os.environ.get("KL_DECODE_PAIRED")
     os.environ["KL_DECODE_PAIRED"] = "0"
     try:
-        single = gpu_ops.paged_decode_attention(*args, k_scale=ks, v_scale=vs)
+        single = gpu_ops.paged_decode_attention(*args, k_scale=ks, v_scale=vs, num_splits=1)
     finally:
         if old is None:
             del os.environ["KL_DECODE_PAIRED"]
@@ -104,17 +110,20 @@ def test_paired_fp8_cache_matches_unpaired(gpu_ops):
     torch.testing.assert_close(paired.cpu(), want, **tolerance(torch.float16))
 
 
-# The balanced schedule (fewer units than CUs, or num_splits=BALANCED) keeps
-# one KV head per 4-wave workgroup: measured on MI355X, pairing there lost
-# 1.7-2.8 us at batch 1-8 and on every FP8 shape and won 2-3 % only on
-# 16-bit long contexts. The switch must leave it bit-identical and correct.
+# The balanced schedule: the planner's choice below 256 units, or requested
+# with num_splits=BALANCED. Batches with units >= 512 (an even KV head count,
+# one head tile) run it in KV-head pairs; smaller ones in single heads, which
+# the pairing switch must leave bit-identical.
 BALANCED_CASES = [
-    # (lens, hq, hkv, head_dim, dtype, num_splits, empty sequences)
-    ([700], 32, 8, 128, torch.float16, None, 0),
-    ([6000, 1, 5, 300, 17, 16, 33, 2048, 15, 1, 4097, 640, 9, 64, 65, 3], 32, 8, 128, torch.float16, None, 2),
-    ("ragged8", 64, 8, 128, torch.bfloat16, None, 0),
-    ("ragged64", 32, 8, 128, torch.float16, -1, 4),
-    ("ragged8", 16, 2, 64, torch.bfloat16, None, 1),
+    # (lens, hq, hkv, head_dim, dtype, num_splits, empty sequences, paired)
+    ([700], 32, 8, 128, torch.float16, None, 0, False),
+    ([6000, 1, 5, 300, 17, 16, 33, 2048, 15, 1, 4097, 640, 9, 64, 65, 3], 32, 8, 128, torch.float16, None, 2, False),
+    ("ragged8", 64, 8, 128, torch.bfloat16, None, 0, False),
+    ("ragged64", 32, 8, 128, torch.float16, -1, 4, True),
+    ("ragged64", 32, 8, 128, torch.bfloat16, -1, 3, True),
+    ("ragged8", 16, 2, 64, torch.bfloat16, None, 1, False),
+    ("ragged128", 16, 4, 64, torch.float16, -1, 2, True),
+    ([65536] + [2048] * 63, 32, 8, 128, torch.float16, -1, 0, True),
 ]
 
 
@@ -123,22 +132,38 @@ def _balanced_lens(spec) -> list[int]:
         return _lens(8, 3000, seed=8)
     if spec == "ragged64":
         return _lens(64, 1500, seed=64)
+    if spec == "ragged128":
+        return _lens(128, 2500, seed=128)
     return list(spec)
 
 
-@pytest.mark.parametrize(("spec", "hq", "hkv", "head_dim", "dtype", "num_splits", "empty"), BALANCED_CASES)
-def test_balanced_schedule_is_unpaired(gpu_ops, spec, hq, hkv, head_dim, dtype, num_splits, empty):
+@pytest.mark.parametrize(("spec", "hq", "hkv", "head_dim", "dtype", "num_splits", "empty", "paired"), BALANCED_CASES)
+def test_balanced_schedule_pairing(gpu_ops, spec, hq, hkv, head_dim, dtype, num_splits, empty, paired):
     lens = _balanced_lens(spec)
     q, kv, _, _ = random_decode_problem(lens, hq, hkv, head_dim, 16, dtype=dtype, device="cuda", poison=float("nan"))
     empties = _empty_rows(len(lens), empty)
     kv.seq_lens[empties] = 0
     kw = {} if num_splits is None else {"num_splits": num_splits}
-    paired, single = _both(gpu_ops, q, kv, **kw)
+    got, single = _both(gpu_ops, q, kv, **kw)
+    if not paired:
+        assert torch.equal(got, single), "the pairing switch changed the single-head balanced schedule"
+    rows = [b for b in range(len(lens)) if b not in empties][:8]
     want = ref.paged_decode_attention(
-        q.cpu(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table.cpu(), kv.seq_lens.cpu()
+        q[rows].cpu(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table[rows].cpu(), kv.seq_lens[rows].cpu()
     )
-    assert torch.equal(paired, single), "the pairing switch changed the balanced schedule"
-    assert torch.isfinite(paired).all(), "non-finite output: a poisoned page or tail leaked in"
-    torch.testing.assert_close(paired, want, **tolerance(dtype))
-    for b in empties:
-        assert not paired[b].any(), "an empty sequence must give zeros"
+    for out in (got, single):
+        assert torch.isfinite(out).all(), "non-finite output: a poisoned page or tail leaked in"
+        torch.testing.assert_close(out[rows], want, **tolerance(dtype))
+        for b in empties:
+            assert not out[b].any(), "an empty sequence must give zeros"
+
+
+@pytest.mark.parametrize(("batch", "ctx", "dtype"), [(64, 1000, torch.float16), (128, 300, torch.bfloat16)])
+def test_paired_balanced_equals_uniform_pairing_on_even_lengths(gpu_ops, batch, ctx, dtype):
+    """Even lengths give every workgroup exactly one pair unit, so the balanced
+    schedule computes what one uniform split computes, bit for bit."""
+    q, kv = device_decode_problem([ctx] * batch, 32, 8, 128, 16, dtype=dtype, seed=batch)
+    balanced = gpu_ops.paged_decode_attention(q, kv.k_cache, kv.v_cache, kv.block_table, kv.seq_lens,
+                                              num_splits=gpu_ops.BALANCED)
+    uniform = gpu_ops.paged_decode_attention(q, kv.k_cache, kv.v_cache, kv.block_table, kv.seq_lens, num_splits=1)
+    assert torch.equal(balanced, uniform)
