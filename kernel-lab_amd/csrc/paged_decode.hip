@@ -105,6 +105,15 @@ constexpr int kBlock = 16;     // tokens per MFMA block
 constexpr int kMaxPlannedSplits = 64;
 constexpr int kMinPagesPerSplit = KL_DECODE_MIN_PAGES;
 constexpr int kMinPagesPerBalancedWg = KL_DECODE_BALANCED_MIN_PAGES;
+// A batch with fewer units than 2 x CUs runs the balanced schedule in KV-head
+// pairs when every workgroup half streams at least kPairMinPages pages and no
+// pair unit is cut into more than kPairMaxSegments segments. Measured on
+// MI355X (fp16/bf16, events): 64/8/128 B=8 ctx 32768 185 -> 176 us, ctx
+// 131072 704 -> 667 us, 32/8/128 B=8 ctx 32768 183 -> 175 us; shorter
+// segments lose to the 8-wave start (B=8 ctx 4096 +1.9 us) and many-way
+// splits to the merge (64/8/128 B=1 ctx 32768, 64 segments: +6 us).
+constexpr int kPairMinPages = 128;
+constexpr int kPairMaxSegments = 16;
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct DecodeArgs {
@@ -921,6 +930,10 @@ __device__ __forceinline__ void list_prefix(const DecodeArgs& a, int units_per_s
   *pages = own;
 }
 
+// Batches of up to 64 * kScanChunks sequences are scanned with all their
+// seq_lens loads in flight at once: one memory round trip at the start.
+constexpr int kScanChunks = 4;
+
 // Where workgroup `wg` starts: its first list position `pos` (wg * per), the
 // first pages-bearing sequence whose units hold it (batch when pos is past the
 // end) and the list position where that sequence's units begin. One pass over
@@ -928,14 +941,14 @@ __device__ __forceinline__ void list_prefix(const DecodeArgs& a, int units_per_s
 struct Start {
   int64_t total, per, pos, base;
   int b;
-  int pages;     // pages of sequence b (when b < batch)
-  int len;       // its length, clamped to max_pages * page_size
-  int wg_empty;  // batch <= 64 * kScanChunks only: sequence `wg` exists and has no pages
+  int pages;  // pages of sequence b (when b < batch)
+  int len;    // its length, clamped to max_pages * page_size
+  // batch <= 64 * kScanChunks only: bit j of empties[k] marks sequence
+  // 64 * k + j as existing, without pages, and zeroed by this workgroup
+  // (sequence b belongs to workgroup b % grid: the grid may be smaller than
+  // the batch when contexts are short).
+  uint64_t empties[kScanChunks];
 };
-
-// Batches of up to 64 * kScanChunks sequences are scanned with all their
-// seq_lens loads in flight at once: one memory round trip at the start.
-constexpr int kScanChunks = 4;
 
 __device__ __forceinline__ int clamped_len(const DecodeArgs& a, int raw) {
   const int64_t cap = static_cast<int64_t>(a.max_pages) * a.page_size;
@@ -949,7 +962,8 @@ __device__ __forceinline__ int pages_of(const DecodeArgs& a, int len) {
 __device__ __forceinline__ Start schedule_start(const DecodeArgs& a, int units_per_seq, int wg) {
   const int lane = __lane_id();
   Start s;
-  s.wg_empty = 0;
+#pragma unroll
+  for (int k = 0; k < kScanChunks; ++k) s.empties[k] = 0;
   s.pages = 0;
   s.len = 0;
   if (a.batch <= 64 * kScanChunks) {
@@ -973,6 +987,8 @@ __device__ __forceinline__ Start schedule_start(const DecodeArgs& a, int units_p
         pl[k] = pages_of(a, len[k]) * units_per_seq;
         incl[k] = wave_incl_scan(pl[k]);
         total += __builtin_amdgcn_readlane(incl[k], 63);
+        const int b = 64 * k + lane;
+        s.empties[k] = __ballot(b < a.batch && pl[k] == 0 && b % a.grid == static_cast<int>(blockIdx.x));
       }
     }
     s.total = total;
@@ -990,9 +1006,6 @@ __device__ __forceinline__ Start schedule_start(const DecodeArgs& a, int units_p
         s.pages = __builtin_amdgcn_readlane(pl[k], j) / units_per_seq;
         s.len = __builtin_amdgcn_readlane(len[k], j);
         found = true;
-      }
-      if (wg >= 64 * k && wg < 64 * k + 64 && wg < a.batch) {
-        s.wg_empty = __builtin_amdgcn_readlane(pl[k], wg - 64 * k) == 0;
       }
     }
   } else {
@@ -1021,7 +1034,6 @@ __device__ __forceinline__ Start schedule_start(const DecodeArgs& a, int units_p
   s.b = __builtin_amdgcn_readfirstlane(s.b);
   s.pages = __builtin_amdgcn_readfirstlane(s.pages);
   s.len = __builtin_amdgcn_readfirstlane(s.len);
-  s.wg_empty = __builtin_amdgcn_readfirstlane(s.wg_empty);
   return s;
 }
 
@@ -1036,11 +1048,34 @@ constexpr int balanced_waves() {
   return D <= 128 ? KL_DECODE_BALANCED_WAVES : kWaves;
 }
 
+// The list workgroup w that hardware workgroup i runs, in KV-head pairs.
+// Workgroups are dealt to the XCDs round robin (i % 8). When each pair unit
+// is cut into m >= 2 segments (m = grid / list units, a power of two dividing
+// the grid here), list order would put a sequence's pairs at the same offset
+// (the workgroups reading the same pages at the same time) on one XCD, and
+// every XCD would serve all pairs. The transposed order w = (i % rows) * m +
+// i / rows (rows = grid / m) makes consecutive i the consecutive pair units
+// at one offset, so XCD x serves pair x % 4 of 8 KV heads, as one workgroup
+// per unit does: measured at 32/8/128 B=8 ctx 32768 (per-workgroup clock
+// stamps), workgroups with equal work end within 155-162 us instead of
+// 138-169 us, and the kernel takes 172-177 instead of 178-179 us. Unpaired
+// balanced launches keep list order (the same order measured within 1 %).
+__device__ __forceinline__ int paired_list_wg(const DecodeArgs& a, int units_per_seq) {
+  const int i = static_cast<int>(blockIdx.x);
+  const int64_t list_units = static_cast<int64_t>(a.batch) * units_per_seq;
+  const int64_t q = list_units > 0 ? a.grid / list_units : 0;
+  if (q < 2) return i;
+  const int m = 1 << (31 - __builtin_clz(static_cast<unsigned>(q)));
+  if (a.grid % m != 0) return i;
+  const int rows = a.grid / m;
+  return (i % rows) * m + i / rows;
+}
+
 // PAIR = 2 (num_kv_heads even): the work list's units are KV-head pairs (j,
 // head group); the workgroup has two halves of W waves that walk the same
 // segments, half h streaming KV head 2j + h with its own LDS (adjacent bytes
 // of every token row, as in decode_mfma_paired_kernel). Half h of segment
-// (w, list unit u) owns partial slot (w + u) * 2 + h.
+// (list workgroup w, list unit u) owns partial slot (w + u) * 2 + h.
 template <typename E, typename KVF, int D, int NT, int PAIR>
 __global__ void __launch_bounds__(PAIR * balanced_waves<D>() * 64, (mfma_waves_per_eu<D, NT>()))
     decode_mfma_balanced_kernel(const DecodeArgs a) {
@@ -1050,16 +1085,20 @@ __global__ void __launch_bounds__(PAIR * balanced_waves<D>() * 64, (mfma_waves_p
   // A compile-time 0 with PAIR == 1, so the LDS base stays a constant.
   const int half = PAIR == 2 ? wave_id() / W : 0;
   const int hp = a.num_kv_heads * a.head_groups / PAIR;  // list units per sequence
-  const Start st = schedule_start(a, hp, blockIdx.x);
+  const int w = PAIR == 2 ? paired_list_wg(a, hp) : static_cast<int>(blockIdx.x);
+  const Start st = schedule_start(a, hp, w);
   if (a.arrivals != nullptr) {
     // No merge kernel follows: empty sequences get their zeros here, sequence
-    // b from workgroup b % grid (a batch of up to 64 from the schedule's scan).
+    // b from workgroup b % grid (up to 64 * kScanChunks from the schedule's scan).
     auto zero = [&](int b) {
       typename E::S* out = static_cast<typename E::S*>(a.out) + static_cast<int64_t>(b) * a.num_q_heads * D;
       for (int i = threadIdx.x; i < a.num_q_heads * D; i += blockDim.x) out[i] = E::from_f32(0.0f);
     };
     if (a.batch <= 64 * kScanChunks) {
-      if (st.wg_empty) zero(blockIdx.x);
+#pragma unroll
+      for (int k = 0; k < kScanChunks; ++k) {
+        for (uint64_t m = st.empties[k]; m != 0; m &= m - 1) zero(64 * k + __builtin_ctzll(m));
+      }
     } else {
       for (int b = blockIdx.x; b < a.batch; b += gridDim.x) {
         if (seq_pages_uniform(a, b) == 0) zero(b);
@@ -1092,7 +1131,7 @@ __global__ void __launch_bounds__(PAIR * balanced_waves<D>() * 64, (mfma_waves_p
     u.page_begin = __builtin_amdgcn_readfirstlane(page0);
     u.page_end = __builtin_amdgcn_readfirstlane(page1);
 
-    const int64_t slot = (static_cast<int64_t>(blockIdx.x) + static_cast<int64_t>(b) * hp + r) * PAIR + half;
+    const int64_t slot = (static_cast<int64_t>(w) + static_cast<int64_t>(b) * hp + r) * PAIR + half;
     Dest dst;
     dst.final = page0 == 0 && page1 == n;
     dst.o = a.o_part + slot * a.heads_per_wg * D;
@@ -1787,9 +1826,14 @@ int make_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads, int 
   const int64_t units = std::max<int64_t>(1, static_cast<int64_t>(batch) * num_kv_heads * p->head_groups);
   if (num_splits == KL_SPLITS_BALANCED && (!mfma || partials)) num_splits = 0;  // uniform splits only
   // The balanced schedule runs in KV-head pairs (8-wave workgroups) on
-  // batches that fill the device twice over, as uniform splits would.
+  // batches that fill the device twice over, as uniform splits would, and on
+  // long contexts that give every workgroup half long segments of few-way
+  // split pair units (kPairMinPages, kPairMaxSegments).
+  const int64_t pair_units = units / 2;
+  const bool long_pairs = pair_units * pages >= static_cast<int64_t>(cus) * kPairMinPages &&
+                          pair_units * kPairMaxSegments >= cus;
   const bool pairable = mfma && !partials && pairing_enabled() && num_kv_heads % 2 == 0 && head_dim <= 128 &&
-                        p->heads_per_wg <= 16 && units >= 2 * static_cast<int64_t>(cus);
+                        p->heads_per_wg <= 16 && (units >= 2 * static_cast<int64_t>(cus) || long_pairs);
   const bool balance = num_splits == KL_SPLITS_BALANCED || (num_splits == 0 && (units < cus || balance_always()));
   const bool pair_balanced = pairable && balance;
   if (mfma && !partials && balance) {

@@ -119,7 +119,8 @@ def test_balanced_planner_on_request(monkeypatch, batch, hkv, max_pages):
     monkeypatch.setenv("KL_DECODE_BALANCE_ALWAYS", "1")
     splits, ws = ops.plan_decode(torch.float16, batch, hkv * 4, hkv, 128, 16, max_pages, 0, 256)
     units = batch * hkv
-    paired = hkv % 2 == 0 and units >= 512
+    long_pairs = units // 2 * max_pages >= 256 * 128 and units // 2 * 16 >= 256
+    paired = hkv % 2 == 0 and (units >= 512 or long_pairs)
     lunits = units // 2 if paired else units
     floor = 256 if paired else max(256, units)
     grid = min(floor, -(-lunits * max_pages // 8))
@@ -128,6 +129,38 @@ def test_balanced_planner_on_request(monkeypatch, batch, hkv, max_pages):
     monkeypatch.setenv("KL_DECODE_BALANCE_ALWAYS", "0")
     uniform = ops.plan_decode(torch.float16, batch, hkv * 4, hkv, 128, 16, max_pages, 0, 256)[0]
     assert uniform >= 1 if units >= 256 else uniform == 0  # fewer units than CUs: balanced regardless
+
+
+def _align(n: int) -> int:
+    return -(-n // 256) * 256
+
+
+@pytest.mark.parametrize(
+    ("batch", "hkv", "max_pages", "paired"),
+    [
+        (8, 8, 2048, True),  # 32 pair units x 2048 pages: 256 pages per workgroup half, 8 segments each
+        (8, 8, 8192, True),
+        (16, 8, 1024, True),
+        (8, 8, 1024, True),  # exactly 128 pages per half
+        (8, 8, 1023, False),
+        (8, 8, 256, False),  # 32 pages per half: the 8-wave start costs more than pairing gains
+        (1, 8, 8192, False),  # 4 pair units: 64 segments each
+        (12, 2, 8192, False),  # 12 pair units: more than 16 segments each
+        (8, 1, 32768, False),  # one KV head: nothing to pair
+    ],
+)
+def test_planner_pairs_long_contexts_of_small_batches(batch, hkv, max_pages, paired):
+    """Fewer units than CUs (balanced by default): the list runs in KV-head
+    pairs when every workgroup half gets >= 128 pages and a pair unit at most
+    16 segments. The workspace is exact: a partial slot per list workgroup and
+    list unit, two per slot when paired."""
+    splits, ws = ops.plan_decode(torch.float16, batch, hkv * 4, hkv, 128, 16, max_pages, 0, 256)
+    units = batch * hkv
+    lunits = units // 2 if paired else units
+    grid = min(256, -(-lunits * max_pages // 8))
+    slots = (grid + lunits) * (2 if paired else 1)
+    assert splits == 0
+    assert ws == _align(slots * 4 * 128 * 4) + _align(slots * 4 * 4)
 
 
 def test_requested_balanced_schedule_at_any_batch():

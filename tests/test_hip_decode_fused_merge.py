@@ -159,6 +159,37 @@ def test_streams_beyond_the_regions_fall_back(gpu_ops):
         assert torch.equal(out, want)
 
 
+@pytest.mark.parametrize(
+    ("batch", "hq", "hkv", "max_len", "splits"),
+    [
+        (64, 8, 2, 32, None),  # 128 units of <= 2 pages: a grid of <= 32 workgroups
+        (256, 32, 8, 16, -1),  # paired balanced on request, one page each: 128 workgroups
+        (300, 8, 2, 16, -1),   # past the schedule's one-pass scan: 38 workgroups
+    ],
+)
+def test_empty_sequences_beyond_the_grid(gpu_ops, batch, hq, hkv, max_len, splits):
+    """Short contexts give a balanced grid smaller than the batch (one
+    workgroup per 8 list pages), so workgroup b cannot zero sequence b: every
+    empty sequence must still get zeros, with an output buffer that starts as
+    NaN, and the rest must equal the merge kernel's result."""
+    lens = _lens(batch, max_len, seed=batch)
+    q, kv = device_decode_problem(lens, hq, hkv, 128, 16, dtype=torch.float16, seed=batch + 1)
+    empty = [1, batch // 2 + 3, batch - 1]
+    kv.seq_lens[empty] = 0
+    kw = {} if splits is None else {"num_splits": splits}
+    fused = _decode(gpu_ops, q, kv, out=torch.full_like(q, float("nan")), **kw).cpu()
+    merged = _unfused(lambda: _decode(gpu_ops, q, kv, out=torch.full_like(q, float("nan")), **kw)).cpu()
+    for b in empty:
+        assert torch.equal(fused[b], torch.zeros_like(fused[b])), f"sequence {b} is empty and must give zeros"
+    assert torch.isfinite(fused).all(), "a row was left unwritten"
+    assert torch.equal(fused, merged)
+    rows = [0, 2, batch // 2, batch - 2]
+    want = ref.paged_decode_attention(
+        q[rows].cpu(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table[rows].cpu(), kv.seq_lens[rows].cpu()
+    )
+    torch.testing.assert_close(fused[rows], want, **tolerance(torch.float16))
+
+
 @pytest.mark.parametrize(("lens", "splits"), [([4096] * 8, None), ([900] * 16, 6), ([30000, 40, 500], None)])
 def test_fresh_partials_every_call(gpu_ops, lens, splits):
     """New queries on every call, so every call's partials differ from the

@@ -13,9 +13,12 @@ workgroup (GQA group 24), head_dim 32 and 64, and the FP8 cache.
 
 The balanced schedule (the planner's choice below 256 units, and what
 ``num_splits=BALANCED`` asks for) runs in KV-head pairs on batches with
-units >= 512 and one head tile: checked against the oracle and the unpaired
-balanced schedule, and, on even lengths (one pair unit per workgroup),
-bit-identical to uniform pairing.
+units >= 512 and one head tile, and on long contexts of small batches (at
+least 128 pages per workgroup half, at most 16 segments per pair unit):
+checked against the oracle and the unpaired balanced schedule, and, on even
+lengths, bit-identical to uniform pairing with the same cut (one pair unit
+per workgroup, or uniform splits of the segment length, whose workgroups the
+balanced kernel runs in transposed order).
 """
 
 from __future__ import annotations
@@ -111,9 +114,9 @@ def test_paired_fp8_cache_matches_unpaired(gpu_ops):
 
 
 # The balanced schedule: the planner's choice below 256 units, or requested
-# with num_splits=BALANCED. Batches with units >= 512 (an even KV head count,
-# one head tile) run it in KV-head pairs; smaller ones in single heads, which
-# the pairing switch must leave bit-identical.
+# with num_splits=BALANCED. Batches with units >= 512 or long contexts (an
+# even KV head count, one head tile) run it in KV-head pairs; others in single
+# heads, which the pairing switch must leave bit-identical.
 BALANCED_CASES = [
     # (lens, hq, hkv, head_dim, dtype, num_splits, empty sequences, paired)
     ([700], 32, 8, 128, torch.float16, None, 0, False),
@@ -124,6 +127,8 @@ BALANCED_CASES = [
     ("ragged8", 16, 2, 64, torch.bfloat16, None, 1, False),
     ("ragged128", 16, 4, 64, torch.float16, -1, 2, True),
     ([65536] + [2048] * 63, 32, 8, 128, torch.float16, -1, 0, True),
+    ([20000] * 8, 32, 8, 128, torch.float16, None, 1, True),  # long contexts of a small batch: paired by default
+    ("ragged16long", 32, 8, 128, torch.bfloat16, None, 2, True),
 ]
 
 
@@ -134,6 +139,8 @@ def _balanced_lens(spec) -> list[int]:
         return _lens(64, 1500, seed=64)
     if spec == "ragged128":
         return _lens(128, 2500, seed=128)
+    if spec == "ragged16long":
+        return _lens(16, 30000, seed=16)
     return list(spec)
 
 
@@ -167,3 +174,28 @@ def test_paired_balanced_equals_uniform_pairing_on_even_lengths(gpu_ops, batch, 
                                               num_splits=gpu_ops.BALANCED)
     uniform = gpu_ops.paged_decode_attention(q, kv.k_cache, kv.v_cache, kv.block_table, kv.seq_lens, num_splits=1)
     assert torch.equal(balanced, uniform)
+
+
+@pytest.mark.parametrize(
+    ("batch", "ctx", "splits", "dtype"),
+    [(8, 16384, 8, torch.float16), (8, 40960, 8, torch.bfloat16), (16, 16384, 4, torch.float16)],
+)
+def test_long_context_pairs_equal_uniform_splits(gpu_ops, batch, ctx, splits, dtype):
+    """A small batch of long, even contexts runs the balanced schedule in
+    KV-head pairs with its workgroups in transposed order; the cut equals
+    uniform splits of the same page count, merged in the same order, so the
+    results are bit-identical to the uniform paired kernel's."""
+    q, kv = device_decode_problem([ctx] * batch, 32, 8, 128, 16, dtype=dtype, seed=ctx)
+    pages = -(-ctx // 16)
+    grid = min(256, -(-batch * 4 * pages // 8))
+    assert (batch * 4 * pages) % grid == 0 and (batch * 4 * pages // grid) * splits == pages, "not the same cut"
+    planned = gpu_ops.paged_decode_attention(q, kv.k_cache, kv.v_cache, kv.block_table, kv.seq_lens)
+    uniform = gpu_ops.paged_decode_attention(q, kv.k_cache, kv.v_cache, kv.block_table, kv.seq_lens,
+                                             num_splits=splits)
+    assert torch.isfinite(planned).all()
+    assert torch.equal(planned, uniform)
+    rows = [0, batch - 1]
+    want = ref.paged_decode_attention(
+        q[rows].cpu(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table[rows].cpu(), kv.seq_lens[rows].cpu()
+    )
+    torch.testing.assert_close(planned[rows].cpu(), want, **tolerance(dtype))
