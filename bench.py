@@ -244,6 +244,10 @@ def main(argv: list[str] | None = None) -> int:
         kernels["paged_decode_attention"] = kernel_entry(dec_work, dec_ms) | {"bytes": dec_work.bytes}
     if do_rms:
         kernels["fused_add_rms_norm"] = kernel_entry(rms_work, rms_ms) | {"bytes": rms_work.bytes}
+    for op, entry in kernels.items():
+        if entry["frac_of_peak"] > 0.92:
+            # The reference runbook's sanity check (docs/gpu-runbook.md:75-76).
+            log(f"warning: {op} above 92 % of peak: check the byte count and cache residency")
 
     dom_work, dom_ms = (dec_work, dec_ms) if do_dec else (rms_work, rms_ms)
     achieved = dom_work.bytes / (dom_ms * 1e-3) / 1e9

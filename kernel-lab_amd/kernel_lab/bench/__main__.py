@@ -88,6 +88,10 @@ class Timer:
         return times[len(times) // 2]
 
 
+# Achieved bandwidth above this fraction of the spec-sheet peak is flagged.
+SUSPECT_FRACTION = 0.92
+
+
 def measure(
     kernel: str,
     shape: str,
@@ -117,9 +121,14 @@ def measure(
         gbps = w.bytes / (us * 1e-6) / 1e9
         if name == baseline:
             base_us = us
+        note = ""
+        if peak and gbps > SUSPECT_FRACTION * peak.dram_gbps:
+            # docs/gpu-runbook.md:75-76 of the reference: a wrong byte count,
+            # or data served from cache instead of HBM.
+            note = "above 92 % of peak: check the byte count and cache residency"
         rows.append(
             Row(kernel, shape, name, round(us, 2), round(gbps, 1),
-                round(100 * gbps / peak.dram_gbps, 1) if peak else None, None, err)
+                round(100 * gbps / peak.dram_gbps, 1) if peak else None, None, err, note)
         )
     for row in rows:
         if row.us and base_us:
@@ -174,6 +183,8 @@ def rmsnorm_suite(dtype: torch.dtype, peak: GPUPeak | None, timer, compile_basel
                     base = next((r.us for r in got if r.impl == "torch eager" and r.us), None)
                     row.speedup = round(base / us, 2) if base else None
                     row.note = "in-place operator"
+                    if peak and row.gbps > SUSPECT_FRACTION * peak.dram_gbps:
+                        row.note += "; above 92 % of peak: check the byte count and cache residency"
             rows += got
     return rows
 

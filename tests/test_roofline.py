@@ -85,6 +85,22 @@ def test_markdown_marks_skips_and_wrong_results():
     assert "bad (WRONG RESULT, not timed)" in text
 
 
+def test_measure_flags_bandwidth_above_92_percent_of_peak():
+    """The reference runbook's sanity check (docs/gpu-runbook.md:75-76): above
+    ~92 % of peak the byte count is wrong or the data came from cache."""
+    import torch
+
+    from kernel_lab.bench.__main__ import measure
+
+    work = roofline.Work(bytes=8e9, flops=0.0)  # 8 GB: 1000 us is 8 TB/s
+    impls = {"base": lambda: torch.zeros(4), "ok": lambda: torch.zeros(4), "suspect": lambda: torch.zeros(4)}
+    times = iter([2000.0, 1100.0, 1050.0])  # 50 %, 90.9 %, 95.2 % of 8 TB/s
+    rows = measure("k", "s", impls, work, roofline.MI355X, "base", 0.0, lambda fn: next(times))
+    notes = {r.impl: r.note for r in rows}
+    assert notes["base"] == "" and notes["ok"] == ""
+    assert "above 92 %" in notes["suspect"]
+
+
 def test_cli_without_gpu_exits_cleanly(capsys):
     import torch
 
