@@ -16,7 +16,14 @@ the measured configurations):
 * cascade: shared-prefix decode against plain paged decode over the same
   pages (prefixes of 4096-32768 tokens shared by 16-64 sequences);
 * copy: a 1 GiB device copy (the streaming ceiling, and the counter
-  calibration kernel for the profiles).
+  calibration kernel for the profiles);
+* configs: each measured configuration's planner call (fused add+RMSNorm at
+  every token count and hidden size in bf16 and fp16, Llama-3-8B decode at
+  batch {1, 8, 32, 64} x context {512, 4096}, ragged MQA, long-context
+  64/8/128), writing ``order.json`` with ``--out``; ``attribute --trace
+  run_kernel_trace.csv --order order.json`` then gives each configuration's
+  median kernel time from a rocprofv3 kernel trace of that run (no GPU
+  needed).
 
 Every implementation is checked against the PyTorch baseline before it is
 timed; a wrong result is reported as such, never as a speed. Timing: HIP
@@ -412,6 +419,129 @@ def copy_suite(peak: GPUPeak | None, timer, mib: int = 1024) -> list[Row]:
     return rows
 
 
+# ------------------------------------------------------- BASELINE configs
+
+WARMUP_CALLS = 3  # Timer's untimed calls before the timed ones
+
+
+def baseline_config_cases() -> list[tuple[str, str, dict]]:
+    """The measured configurations, in a fixed order: (config, label, spec)."""
+    cases = []
+    for dt in (torch.bfloat16, torch.float16):
+        for hidden in (4096, 8192):
+            for tokens in (1, 16, 128, 1024, 4096):
+                cases.append(("cfg1", f"{str(dt)[6:]} {tokens}x{hidden}",
+                              {"kind": "rms", "tokens": tokens, "hidden": hidden, "dtype": dt}))
+    for batch in (1, 8, 32, 64):
+        for ctx in (512, 4096):
+            cases.append(("cfg2", f"32/8/128 fp16 B={batch} ctx {ctx}",
+                          {"kind": "decode", "lens": [ctx] * batch, "hq": 32, "hkv": 8, "dtype": torch.float16}))
+    g = torch.Generator().manual_seed(3)
+    ragged = torch.randint(1, 8193, (64,), generator=g).tolist()
+    cases.append(("cfg3", "32/1/128 bf16 B=64 L~U[1,8192]",
+                  {"kind": "decode", "lens": ragged, "hq": 32, "hkv": 1, "dtype": torch.bfloat16}))
+    for ctx in (32768, 131072):
+        cases.append(("cfg4", f"64/8/128 bf16 B=8 ctx {ctx}",
+                      {"kind": "decode", "lens": [ctx] * 8, "hq": 64, "hkv": 8, "dtype": torch.bfloat16}))
+    return cases
+
+
+def configs_suite(peak: GPUPeak | None, timer, shape: str | None = None) -> tuple[list[Row], list[dict]]:
+    """Each measured configuration's planner call: checked once against the
+    PyTorch computation, then timed (WARMUP_CALLS + reps calls). The second
+    result lists the cases in launch order with their call counts, so a
+    rocprofv3 kernel trace of this run can be attributed (``attribute``)."""
+    rows: list[Row] = []
+    order: list[dict] = []
+    for cfg, label, spec in baseline_config_cases():
+        if shape and shape not in label:
+            continue
+        dt = spec["dtype"]
+        elem = torch.tensor([], dtype=dt).element_size()
+        if spec["kind"] == "rms":
+            gen = torch.Generator(device="cuda").manual_seed(spec["tokens"] + spec["hidden"])
+            x = torch.randn(spec["tokens"], spec["hidden"], generator=gen, device="cuda").to(dt)
+            r = torch.randn(spec["tokens"], spec["hidden"], generator=gen, device="cuda").to(dt)
+            w = (1 + 0.1 * torch.randn(spec["hidden"], generator=gen, device="cuda")).to(dt)
+            out = torch.empty_like(x)
+            res = r.clone()
+            s = x + r
+            expected = torch.nn.functional.rms_norm(s, (s.shape[-1],), w, eps=1e-6)
+            fn = lambda x=x, w=w, out=out, res=res: torch.ops.kernel_lab.fused_add_rms_norm(out, x, res, w, 1e-6)
+            work = rms_norm_work(spec["tokens"], spec["hidden"], elem, fused_residual=True)
+            kernel = "fused_add_rms_norm"
+        else:
+            q, kv = device_decode_problem(spec["lens"], spec["hq"], spec["hkv"], 128, 16, dtype=dt, device="cuda")
+            out = torch.empty_like(q)
+            args = (q, kv.k_cache, kv.v_cache, kv.block_table, kv.seq_lens)
+            scale = 128 ** -0.5
+            expected = torch_paged_decode(*args, scale)
+            fn = lambda a=args, o=out: ops.paged_decode_attention(*a, scale, out=o)
+            work = decode_attention_work(spec["lens"], spec["hq"], spec["hkv"], 128, elem)
+            kernel = "paged_decode"
+        fn()
+        err = (out.float() - expected.float()).abs().max().item()
+        atol = 2e-2
+        if not err <= atol:
+            rows.append(Row(kernel, f"{cfg} {label}", "hip (planner)", None, None, None, None, err,
+                            "WRONG RESULT, not timed"))
+            order.append({"cfg": cfg, "case": label, "calls": 1, "bytes": work.bytes})
+            continue
+        us = timer(fn)
+        gbps = work.bytes / (us * 1e-6) / 1e9
+        pct = round(100 * gbps / peak.dram_gbps, 1) if peak else None
+        rows.append(Row(kernel, f"{cfg} {label}", "hip (planner)", round(us, 2), round(gbps, 1), pct, None, err))
+        order.append({"cfg": cfg, "case": label, "calls": 1 + WARMUP_CALLS + timer.reps, "timed": timer.reps,
+                      "bytes": work.bytes})
+        del expected, out
+        torch.cuda.empty_cache()
+    return rows, order
+
+
+# Kernels of this library in a kernel trace: the main launch of a call, and the
+# merge launches that follow it in the same call.
+_MAIN_KERNELS = ("decode_mfma", "decode_valu", "rms_norm")
+_MERGE_KERNELS = ("decode_merge", "cascade_merge")
+
+
+def attribute_trace(trace_csv: Path, order: list[dict]) -> str:
+    """Median kernel time per case from a rocprofv3 ``--kernel-trace`` CSV of
+    a ``configs`` run: the library's dispatches in start order are its calls
+    (a main kernel plus any merge kernel), the cases' call counts cut them
+    into cases, and each case's last ``timed`` calls give the medians."""
+    import csv
+    import statistics
+
+    with open(trace_csv) as f:
+        recs = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    calls: list[list] = []  # [kernel, main ns, merge ns]
+    for r in recs:
+        name = r["Kernel_Name"].replace("void kl::(anonymous namespace)::", "").split("(kl::")[0].replace("kl::", "")
+        dur = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+        if any(k in name for k in _MAIN_KERNELS):
+            calls.append([name, dur, 0])
+        elif any(k in name for k in _MERGE_KERNELS) and calls:
+            calls[-1][2] += dur
+    need = sum(c["calls"] for c in order)
+    if len(calls) != need:
+        raise ValueError(f"trace holds {len(calls)} calls of this library, the run made {need}")
+    lines = [
+        "| config | case | kernel | kernel µs | merge µs | algorithmic bytes | GB/s | % of peak |",
+        "|---|---|---|---:|---:|---:|---:|---:|",
+    ]
+    i = 0
+    for c in order:
+        grp = calls[i : i + c["calls"]][-c.get("timed", 1):]
+        i += c["calls"]
+        main_ns = statistics.median(g[1] for g in grp)
+        merge_ns = statistics.median(g[2] for g in grp)
+        kernels = ", ".join(sorted({g[0] for g in grp}))
+        gbps = c["bytes"] / (main_ns + merge_ns)
+        lines.append(f"| {c['cfg']} | {c['case']} | {kernels} | {main_ns / 1e3:,.1f} | {merge_ns / 1e3:,.1f} | "
+                     f"{c['bytes']:,} | {gbps:,.0f} | {100 * gbps / 8000:.1f} |")
+    return "\n".join(lines) + "\n"
+
+
 # --------------------------------------------------------------------- report
 
 
@@ -437,7 +567,8 @@ def main(argv: list[str] | None = None) -> int:
     parser = argparse.ArgumentParser(
         prog="python -m kernel_lab.bench", description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter
     )
-    parser.add_argument("suite", choices=["rmsnorm", "decode", "decode-fp8", "cascade", "copy", "all"])
+    parser.add_argument("suite", choices=["rmsnorm", "decode", "decode-fp8", "cascade", "copy", "configs",
+                                          "attribute", "all"])
     parser.add_argument("--dtype", choices=list(DTYPES), default="float16")
     parser.add_argument("--peak-gbps", type=float, help="override the spec-sheet DRAM bandwidth")
     parser.add_argument("--compile", action="store_true", help="add the torch.compile RMSNorm baseline")
@@ -447,7 +578,16 @@ def main(argv: list[str] | None = None) -> int:
     parser.add_argument("--baseline-max-gb", type=float, default=8.0, help="skip the gather baseline above this")
     parser.add_argument("--out", type=Path, help="directory for results.json and results.md")
     parser.add_argument("--shape", help="run only the cases whose shape label contains this text")
+    parser.add_argument("--trace", type=Path, help="attribute: a rocprofv3 kernel_trace.csv of a configs run")
+    parser.add_argument("--order", type=Path, help="attribute: the configs run's order.json")
     args = parser.parse_args(argv)
+
+    if args.suite == "attribute":  # no GPU needed
+        if not args.trace or not args.order:
+            print("attribute needs --trace and --order", file=sys.stderr)
+            return 2
+        print(attribute_trace(args.trace, json.loads(args.order.read_text())), end="")
+        return 0
 
     if not torch.cuda.is_available():
         print("No GPU device: the benchmarks need an AMD Instinct GPU (MI355X).", file=sys.stderr)
@@ -477,6 +617,10 @@ def main(argv: list[str] | None = None) -> int:
         rows += cascade_suite(peak, timer, args.shape)
     if args.suite == "copy":
         rows += copy_suite(peak, timer)
+    order = None
+    if args.suite == "configs":
+        got, order = configs_suite(peak, timer, args.shape)
+        rows += got
 
     header = (
         f"### {name} ({arch}), {args.dtype}\n\nPeak DRAM bandwidth used for %: "
@@ -491,6 +635,8 @@ def main(argv: list[str] | None = None) -> int:
                 "peak_dram_gbps": peak.dram_gbps if peak else None, "flush_mb": args.flush_mb, "reps": args.reps}
         (args.out / "results.json").write_text(json.dumps({"meta": meta, "rows": [asdict(r) for r in rows]}, indent=2))
         (args.out / "results.md").write_text(table)
+        if order is not None:
+            (args.out / "order.json").write_text(json.dumps(order, indent=2))
     return 0
 
 

@@ -123,3 +123,69 @@ def test_decode_cases_cover_the_measured_configs():
     ragged = next(c for c in decode_cases(torch.float16) if "ragged" in c[0])
     assert ragged[2:] == (32, 1, torch.bfloat16) and len(ragged[1]) == 64
     assert 1 <= min(ragged[1]) and max(ragged[1]) <= 8192
+
+
+def test_config_cases_cover_every_measured_config():
+    """The configs suite runs every measured configuration: cfg1 (fused
+    add+RMSNorm, bf16 and fp16, tokens {1, 16, 128, 1024, 4096} x hidden
+    {4096, 8192}), cfg2 (32/8/128 fp16, B {1, 8, 32, 64} x ctx {512, 4096}),
+    cfg3 (ragged MQA) and cfg4 (64/8/128 bf16 B=8, ctx 32768 and 131072)."""
+    import torch
+
+    from kernel_lab.bench.__main__ import baseline_config_cases
+
+    cases = baseline_config_cases()
+    by_cfg = {}
+    for cfg, _, spec in cases:
+        by_cfg.setdefault(cfg, []).append(spec)
+    assert len(by_cfg["cfg1"]) == 20
+    assert {(s["tokens"], s["hidden"]) for s in by_cfg["cfg1"]} == {
+        (t, h) for t in (1, 16, 128, 1024, 4096) for h in (4096, 8192)
+    }
+    assert {(len(s["lens"]), s["lens"][0]) for s in by_cfg["cfg2"]} == {
+        (b, c) for b in (1, 8, 32, 64) for c in (512, 4096)
+    }
+    (mqa,) = by_cfg["cfg3"]
+    assert (mqa["hq"], mqa["hkv"], mqa["dtype"], len(mqa["lens"])) == (32, 1, torch.bfloat16, 64)
+    assert {s["lens"][0] for s in by_cfg["cfg4"]} == {32768, 131072}
+    assert all(s["hq"] == 64 and s["hkv"] == 8 and len(s["lens"]) == 8 for s in by_cfg["cfg4"])
+
+
+def test_attribute_trace_assigns_calls_in_order(tmp_path):
+    """Dispatches of other kernels are skipped, a merge kernel is added to the
+    call before it, and each case's medians come from its last timed calls."""
+    from kernel_lab.bench.__main__ import attribute_trace
+
+    rows = []
+    t = 0
+
+    def dispatch(name, dur):
+        nonlocal t
+        rows.append((name, t, t + dur))
+        t += dur + 100
+
+    flush = "void at::native::reduce_kernel<512, 1>(float)"
+    # Case A: 4 calls (1 check + 1 warm-up + 2 timed), one kernel each.
+    for dur in (9_000, 8_000, 5_000, 7_000):
+        dispatch(flush, 50_000)
+        dispatch("void kl::(anonymous namespace)::decode_mfma_kernel<kl::F16, kl::F16, 128, 1>"
+                 "(kl::(anonymous namespace)::DecodeArgs)", dur)
+    # Case B: 3 calls (check + 2 timed), each a decode kernel then a merge kernel.
+    for dur, merge in ((20_000, 9_000), (10_000, 2_000), (12_000, 4_000)):
+        dispatch("void kl::(anonymous namespace)::decode_mfma_balanced_kernel<kl::BF16, kl::BF16, 128, 2, 1>"
+                 "(kl::(anonymous namespace)::DecodeArgs)", dur)
+        dispatch("void kl::(anonymous namespace)::decode_merge_balanced_kernel<kl::BF16>"
+                 "(kl::(anonymous namespace)::DecodeArgs, int)", merge)
+    path = tmp_path / "run_kernel_trace.csv"
+    path.write_text("Kernel_Name,Start_Timestamp,End_Timestamp\n" +
+                    "".join(f'"{n}",{s},{e}\n' for n, s, e in reversed(rows)))
+    order = [
+        {"cfg": "cfgA", "case": "a", "calls": 4, "timed": 2, "bytes": 48_000},
+        {"cfg": "cfgB", "case": "b", "calls": 3, "timed": 2, "bytes": 28_000},
+    ]
+    table = attribute_trace(path, order).splitlines()
+    assert table[2] == "| cfgA | a | decode_mfma_kernel<F16, F16, 128, 1> | 6.0 | 0.0 | 48,000 | 8 | 0.1 |"
+    assert table[3] == ("| cfgB | b | decode_mfma_balanced_kernel<BF16, BF16, 128, 2, 1> | 11.0 | 3.0 | "
+                        "28,000 | 2 | 0.0 |")
+    with pytest.raises(ValueError, match="trace holds"):
+        attribute_trace(path, order[:1])
