@@ -659,6 +659,15 @@ constexpr int kArrivalCounters = 8192;   // units per region
 // than the merge kernel (52.4 vs 49.8 us), and the merge code alone slowed
 // the two-tile kernel's main loop (46 -> 50 us), so those keep the merge kernel.
 constexpr int kFusedMergeMaxHeads = 8;
+// The last arriver's four waves merge the unit serially: each takes
+// cdiv(heads, 4) heads of `segments` partials, where the merge kernel gives
+// every (sequence, head) its own wave. Measured on MI355X (events, fused vs
+// merge kernel), by heads per wave x segments: 16-32 faster (32/8/128 B=1
+// ctx 4096 16.8 vs 18.2 us, ctx 32768 35.3 vs 37.3), 64 even (37.5 vs 36.4),
+// 128-512 slower (8/1/128 B=1 ctx 8192 22.6 vs 18.1, 32/4/128 B=1 ctx 32768
+// 31.9 vs 28.0, 8/1/128 B=1 ctx 32768 54.5 vs 28.7): few units split over
+// the whole device keep the merge kernel.
+constexpr int kFusedMergeMaxWork = 32;
 
 __device__ uint32_t g_decode_arrivals[kArrivalRegions * kArrivalCounters];
 
@@ -1746,6 +1755,11 @@ uint32_t* arrival_region(hipStream_t stream) {
 uint32_t* fused_merge_counters(const DecodeArgs& a, int64_t units, hipStream_t stream) {
   if (!fused_merge_enabled() || units > kArrivalCounters || a.heads_per_wg > kFusedMergeMaxHeads) return nullptr;
   if (a.q_fold != a.group || a.force_partial) return nullptr;  // cascade passes keep their own merge
+  // Segments per unit: the split count, or for the balanced schedule the
+  // workgroups per list unit on even lengths.
+  const int64_t list_units = std::max<int64_t>(1, a.grid > 0 && a.paired ? units / 2 : units);
+  const int64_t segments = a.grid > 0 ? cdiv(a.grid, list_units) : a.num_splits;
+  if (cdiv(a.heads_per_wg, kWaves) * segments > kFusedMergeMaxWork) return nullptr;
   return arrival_region(stream);
 }
 

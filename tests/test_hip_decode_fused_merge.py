@@ -2,8 +2,9 @@
 
 On the MFMA path, a unit split over several segments (uniform splits, or a
 balanced-schedule workgroup range) with one head tile of at most 8 query
-heads is merged by its last segment to finish (MQA and other two-tile units
-keep the merge kernel, and are checked here too), counted on library-owned arrival counters of a
+heads is merged by its last segment to finish (MQA and other two-tile units,
+and units split so widely that the last segment's merge would be long, keep
+the merge kernel, and are checked here too), counted on library-owned arrival counters of a
 region that belongs to the call's stream. The merge is the merge kernels' own
 routine, so every output must be bit-identical with the fused merge switched
 off (``KL_DECODE_FUSED_MERGE=0``), and match the oracle. The counters must be
@@ -61,6 +62,8 @@ CASES = [
     ("m64", 32, 1, 128, torch.bfloat16, None, [9]),  # MQA: 32-head units (merge kernel), balanced
     ([6000, 30, 2500, 800], 32, 1, 64, torch.float16, 7, []),  # MQA, uniform splits, head_dim 64
     ([3000] * 4, 96, 4, 128, torch.float16, None, []),  # 24 heads per unit (two head tiles)
+    ([32768], 8, 1, 128, torch.float16, None, []),  # one unit over 256 workgroups: the merge kernel
+    ([2048], 8, 1, 128, torch.float16, None, []),  # one unit over 16 workgroups: merged in-kernel
 ]
 
 
