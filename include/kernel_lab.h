@@ -123,7 +123,9 @@ int kl_paged_decode_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_
  * NULL when that is 0. batch == 0 is a successful no-op.
  *
  * Split sequences are merged inside the decode kernel where the path allows
- * it (fp16/bf16, at most 8 query heads per KV head and head group): the
+ * it (fp16/bf16, at most 8 query heads per KV head and head group, and a
+ * sequence cut into few enough segments that one workgroup's merge stays
+ * short; otherwise a separate merge launch runs): the
  * library keeps per-device arrival counters (512 KiB) in 16 regions, each
  * taken by the first stream that needs one and reused by that stream's later
  * calls, which the stream runs one after another. A call on a stream beyond
