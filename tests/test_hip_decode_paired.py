@@ -199,3 +199,32 @@ def test_long_context_pairs_equal_uniform_splits(gpu_ops, batch, ctx, splits, dt
         q[rows].cpu(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table[rows].cpu(), kv.seq_lens[rows].cpu()
     )
     torch.testing.assert_close(planned[rows].cpu(), want, **tolerance(dtype))
+
+
+@pytest.mark.parametrize(
+    ("lens_spec", "head_dim", "page_size", "dtype", "empty"),
+    [
+        ("even", 64, 64, torch.float16, []),  # 8 x 1875 pages of 64 tokens, head_dim 64
+        ("ragged", 128, 32, torch.bfloat16, [2, 5]),  # ragged long contexts, empty sequences
+    ],
+)
+def test_long_context_pairs_other_pages_and_head_dims(gpu_ops, lens_spec, head_dim, page_size, dtype, empty):
+    """The long-context pairing rule at other page sizes and head dims: paired
+    (planner default), against the unpaired balanced schedule and the oracle,
+    with empty sequences zeroed."""
+    lens = [120000] * 8 if lens_spec == "even" else _lens(8, 150000, seed=21)
+    pages = -(-max(lens) // page_size)
+    assert len(lens) * 8 // 2 * pages >= 128 * 256, "not a long-context pairing shape (128 pages per half)"
+    q, kv = device_decode_problem(lens, 32, 8, head_dim, page_size, dtype=dtype, seed=page_size)
+    if empty:
+        kv.seq_lens[empty] = 0
+    got, single = _both(gpu_ops, q, kv)
+    rows = [b for b in range(len(lens)) if b not in empty][:3]
+    want = ref.paged_decode_attention(
+        q[rows].cpu(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table[rows].cpu(), kv.seq_lens[rows].cpu()
+    )
+    for out in (got, single):
+        assert torch.isfinite(out).all()
+        torch.testing.assert_close(out[rows], want, **tolerance(dtype))
+        for b in empty:
+            assert not out[b].any(), "an empty sequence must give zeros"
