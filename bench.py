@@ -92,18 +92,26 @@ def check_outputs(q, kv, out, x, res_before, res_after, w, y) -> dict:
 
     rows = [0, 17, 63]
     sub_bt = kv.block_table[rows].cpu()
-    want = ref.paged_decode_attention(
-        q[rows].cpu(), kv.k_cache.cpu(), kv.v_cache.cpu(), sub_bt, kv.seq_lens[rows].cpu(), DECODE["head_dim"] ** -0.5
+    want32 = ref.paged_decode_attention(
+        q[rows].cpu().float(), kv.k_cache.cpu(), kv.v_cache.cpu(), sub_bt, kv.seq_lens[rows].cpu(),
+        DECODE["head_dim"] ** -0.5,
     )
+    want = want32.to(q.dtype)
     got = out[rows].cpu()
     dec_err = (got.float() - want.float()).abs().max().item()
     torch.testing.assert_close(got, want, atol=2e-3, rtol=2e-3)
+    # Distance to the unrounded float32 result in fp16 ulps of that result
+    # (0.5 is a correctly rounded output of the same float32 value).
+    _, e = torch.frexp(want32.double().abs())
+    ulp = torch.pow(2.0, torch.clamp(e.double() - 11, min=-24))
+    dec_ulps = ((got.double() - want32.double()).abs() / ulp).max().item()
     sel = torch.tensor([0, 1, 2047, 4095])
     ref_y, ref_res = ref.fused_add_rms_norm(x[sel].cpu(), res_before[sel].cpu(), w.cpu())
     assert torch.equal(res_after[sel].cpu(), ref_res), "residual not bit-exact"
     rms_err = (y[sel].cpu().float() - ref_y.float()).abs().max().item()
     torch.testing.assert_close(y[sel].cpu(), ref_y, atol=1.6e-2, rtol=1.6e-2)
-    return {"decode_max_abs_err": dec_err, "rmsnorm_max_abs_err": rms_err}
+    return {"decode_max_abs_err": dec_err, "decode_max_err_ulps_vs_fp32": round(dec_ulps, 3),
+            "rmsnorm_max_abs_err": rms_err}
 
 
 def cpu_baseline(q, kv, x, res, w, dec_bytes: float, rms_bytes: float, budget_s: float) -> dict:

@@ -30,11 +30,13 @@
 //                   K is loaded row-coalesced (16 lanes read one token's head
 //                   dims), restaged through a per-wave LDS tile and read back
 //                   as the A operand (lane = token, 8 consecutive head dims).
-//   O^T += V^T P^T  v_mfma_f32_16x16x16_{f16,bf16}: the score tile's output
-//                   layout (lane = head, 4 consecutive tokens) is exactly the
-//                   B operand layout, so P never leaves registers. V is loaded
-//                   the same row-coalesced way, staged in LDS and read back
-//                   transposed (ds_read_b64_tr_b16) as the A operand.
+//   O^T += V^T P^T  v_mfma_f32_16x16x32_{f16,bf16}: the score tile's output
+//                   layout (lane = head, 4 consecutive tokens) is the B operand
+//                   layout, so P never leaves registers; P goes in as a 16-bit
+//                   high part and low part (k = the block's tokens twice), so
+//                   the weights keep ~17-21 bits. V is loaded the same
+//                   row-coalesced way, staged in LDS and read back transposed
+//                   (ds_read_b64_tr_b16) as the A operand.
 // Every K/V element is read from HBM once per unit and used by the whole GQA
 // group. Tokens past seq_len inside the last page are excluded by selects
 // (scores to -inf, V rows to zero), never by multiplying by zero, so NaN or
@@ -233,32 +235,46 @@ __device__ void write_zero_heads(const DecodeArgs& a, const Unit& u, int head_di
 
 // ------------------------------------------------------------ MFMA split path
 
+// 16x16x32 products: lane l holds A[row l % 16][k in group l / 16] and
+// B[k in group l / 16][col l % 16], eight k values each; element e of a lane's
+// A operand meets element e of the B operand of the lane with the same k group.
 template <typename E>
 struct Mfma;
 
 template <>
 struct Mfma<F16> {
-  static __device__ __forceinline__ f32x4 qk(u32x4 a, u32x4 b, f32x4 c) {
+  static __device__ __forceinline__ f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
                                                   0, 0, 0);
-  }
-  static __device__ __forceinline__ f32x4 pv(u32x2 a, u32x2 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c, 0,
-                                                 0, 0);
   }
 };
 
 template <>
 struct Mfma<BF16> {
-  static __device__ __forceinline__ f32x4 qk(u32x4 a, u32x4 b, f32x4 c) {
+  static __device__ __forceinline__ f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
                                                    c, 0, 0, 0);
   }
-  static __device__ __forceinline__ f32x4 pv(u32x2 a, u32x2 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4, a),
-                                                     __builtin_bit_cast(bf16x4, b), c, 0, 0, 0);
-  }
 };
+
+// O^T += V^T (P_hi + P_lo)^T over one 16-token block in one 16x16x32 product.
+// The softmax weights P are fp32; one 16-bit value keeps 8 (bf16) or 11
+// (fp16) of their bits, which left outputs near zero several ulps from the
+// float32 result. P is carried as a pair: P_hi = E(P) and P_lo = E(P - P_hi)
+// (P - P_hi is exact in fp32), good to about 2^-17 of P in bf16 and 2^-21 in
+// fp16. The k dimension holds each lane's four tokens twice: V rows against
+// P_hi, then the same V rows against P_lo. `v` holds V^T[dim][tokens 4g ..
+// 4g+3] (the transposing LDS read), `p_hi` / `p_lo` P[tokens 4g .. 4g+3][head].
+template <typename E>
+__device__ __forceinline__ f32x4 pv_split(u32x2 v, u32x2 p_hi, u32x2 p_lo, f32x4 c) {
+  return Mfma<E>::mma(u32x4{v[0], v[1], v[0], v[1]}, u32x4{p_hi[0], p_hi[1], p_lo[0], p_lo[1]}, c);
+}
+
+// The low part of a packed pair of weights: E(p - f32(E(p))) for both halves.
+template <typename E>
+__device__ __forceinline__ uint32_t pack2_residual(float a, float b, uint32_t hi) {
+  return pack2<E>(a - lo_f32<E>(hi), b - hi_f32<E>(hi));
+}
 
 // LDS bytes the MFMA kernel needs: the per-wave K and V staging tiles during
 // the main loop, reused for the cross-wave merge afterwards.
@@ -282,11 +298,12 @@ struct MfmaLds {
 // (one being processed, the rest in flight); 8 KiB per block at D = 128 with
 // a 16-bit cache, 4 KiB with FP8. Measured on MI355X at D = 128: 2 stages
 // beat 3..6 for both cache formats (FP8 B=64 ctx 4096: 103 us at 2 stages,
-// 107-110 us at 3-6).
-template <int D>
+// 107-110 us at 3-6). At D = 64 two head tiles take 4 stages: with 6 the
+// balanced kernel needs more than its 256 registers and spills.
+template <int D, int NT>
 constexpr int mfma_stages() {
   if (KL_DECODE_STAGES > 0) return KL_DECODE_STAGES;
-  return D <= 64 ? 6 : 2;
+  return D <= 64 ? (NT == 2 ? 4 : 6) : 2;
 }
 
 // Occupancy floor (waves per SIMD) handed to the register allocator. With two
@@ -344,7 +361,7 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
   static_assert(TPL <= kBlock && kBlock % TPL == 0, "a load must stay inside its 16-token block");
   constexpr int KROW = MfmaLds<D, NT, W>::kKRow;
   constexpr int VROW = MfmaLds<D, NT, W>::kVRow;
-  constexpr int NS = mfma_stages<D>();
+  constexpr int NS = mfma_stages<D, NT>();
 
   const int lane = __lane_id();
   const int row = lane & 15;  // MFMA row / column index of this lane
@@ -468,14 +485,14 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
     for (int c = 0; c < KC; ++c) ka[c] = *reinterpret_cast<const u32x4*>(k_src + 32 * c);
 
     // Scores: lane holds S[token 4grp + i][head row] for tile t.
-    u32x2 pf[NT];
+    u32x2 pf[NT], pl[NT];
     float alpha[NT];
     bool grew = false;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int c = 0; c < KC; ++c) s = M::qk(ka[c], qf[t][c], s);
+      for (int c = 0; c < KC; ++c) s = M::mma(ka[c], qf[t][c], s);
       float sc[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) sc[j] = (4 * grp + j < nvalid) ? s[j] * qk_scale : -INFINITY;
@@ -492,6 +509,7 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
       l[t] = l[t] * alpha[t] + ((p[0] + p[1]) + (p[2] + p[3]));
       m[t] = m_new;
       pf[t] = u32x2{pack2<E>(p[0], p[1]), pack2<E>(p[2], p[3])};
+      pl[t] = u32x2{pack2_residual<E>(p[0], p[1], pf[t][0]), pack2_residual<E>(p[2], p[3], pf[t][1])};
     }
     // Rescale the outputs only when some head's running max moved (alpha < 1).
     if (__any(grew)) {
@@ -516,7 +534,7 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
     for (int dt = 0; dt < DT; ++dt) {
       const u32x2 va = lds_read_tr16(tr_src + 16 * dt);
 #pragma unroll
-      for (int t = 0; t < NT; ++t) acc[t][dt] = M::pv(va, pf[t], acc[t][dt]);
+      for (int t = 0; t < NT; ++t) acc[t][dt] = pv_split<E>(va, pf[t], pl[t], acc[t][dt]);
     }
   };
 

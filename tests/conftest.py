@@ -57,6 +57,75 @@ def ulp_distance(a: torch.Tensor, b: torch.Tensor) -> int:
     return int((ai - bi).abs().max()) if ai.numel() else 0
 
 
+# Significand bits (implicit bit included) and the exponent of the smallest
+# subnormal spacing, per storage dtype.
+_FORMAT = {torch.float16: (11, -24), torch.bfloat16: (8, -133), torch.float32: (24, -149)}
+
+
+def ulp_of(x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """Spacing of `dtype` values around |x| (float64): for |x| in
+    [2^(e-1), 2^e) it is 2^(e - p) with p significand bits, floored at the
+    subnormal spacing (which is also what 0 gets)."""
+    p, emin = _FORMAT[dtype]
+    mag = x.double().abs()
+    _, e = torch.frexp(mag)
+    exp = torch.where(mag == 0, torch.full_like(mag, emin), torch.clamp(e.double() - p, min=emin))
+    return torch.pow(torch.tensor(2.0, dtype=torch.float64), exp)
+
+
+# Decode parity against the unrounded float32 oracle: per element,
+#   |got - want| <= DECODE_ULPS * ulp(|want|) + DECODE_FLOOR + DECODE_ROW_REL * rms(row)
+# where the row is the (sequence, head) output vector. A correctly rounded
+# kernel whose fp32 result equals the oracle's is at most half an ulp away, so
+# one ulp leaves half an ulp for the fp32 arithmetic of both sides. Outputs
+# near zero have a tiny ulp while the arithmetic error there is set by the
+# row's scale: the kernel's softmax weights are good to 2^-18 (bf16 high/low
+# pair), and float32 exp2 arguments of size ~10 cost ~1e-6 of relative error,
+# both multiplied by values of the row's magnitude; hence the row term, and an
+# absolute floor for rows that are tiny. Decode outputs shrink as the context
+# grows (rms about 0.026 at 4,096 N(0,1) tokens, 0.005 at 131,072), so an
+# absolute tolerance alone stops seeing errors there; this bound does not: a
+# lost segment of a 16-way split moves outputs by about rms / 4.
+DECODE_ULPS = 1
+DECODE_FLOOR = 1e-6
+DECODE_ROW_REL = 2.0**-16
+
+
+def decode_parity(got: torch.Tensor, want: torch.Tensor, dtype: torch.dtype, what: str = "") -> dict:
+    """Check a decode output against the unrounded oracle `want` (float32 or
+    float64). Two gates: the original project's tolerance table against the
+    oracle rounded to `dtype` (tests/conftest.py:34-39 there), and the
+    magnitude-aware ulp bound above. Returns the measured worst cases."""
+    got = got.detach().cpu()
+    want = want.detach().cpu()
+    assert got.dtype == dtype, (got.dtype, dtype)
+    assert got.shape == want.shape, (got.shape, want.shape)
+    assert torch.isfinite(got).all(), f"{what}: non-finite output: a poisoned page or tail leaked in"
+    rounded = want.to(dtype)
+    torch.testing.assert_close(got, rounded, **tolerance(dtype), msg=lambda m: f"{what}: {m}")
+    err = (got.double() - want.double()).abs()
+    ulp = ulp_of(want, dtype)
+    row_rms = want.double().square().mean(dim=-1, keepdim=True).sqrt() if want.dim() else want.double().abs()
+    bound = DECODE_ULPS * ulp + DECODE_FLOOR + DECODE_ROW_REL * row_rms
+    ratio = err / bound
+    worst = int(ratio.argmax()) if ratio.numel() else 0
+    stats = {
+        "max_ulp_vs_rounded": ulp_distance(got, rounded),
+        "max_err_in_ulps": float((err / ulp).max()) if err.numel() else 0.0,
+        "max_err_over_bound": float(ratio.max()) if ratio.numel() else 0.0,
+    }
+    if stats["max_err_over_bound"] > 1.0:
+        idx = tuple(int(i) for i in torch.unravel_index(torch.tensor(worst), err.shape))
+        raise AssertionError(
+            f"{what}: decode output off the unrounded oracle by more than {DECODE_ULPS} ulp + {DECODE_FLOOR} "
+            f"+ 2^-16 rms(row): "
+            f"at {idx} got {float(got[idx])!r}, want {float(want[idx])!r}, err {float(err[idx]):.3e}, "
+            f"bound {float(bound[idx]):.3e}; {stats}"
+        )
+    print(f"decode parity {what}: {stats}")
+    return stats
+
+
 @pytest.fixture(autouse=True)
 def _seeded_global_rng():
     """Every test starts from the same global torch seed, so draws that do not

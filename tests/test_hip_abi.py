@@ -12,7 +12,7 @@ import torch
 from kernel_lab import _native
 from kernel_lab.kv_cache import random_decode_problem
 from oracle import reference as ref
-from tests.conftest import tolerance
+from tests.conftest import decode_parity, tolerance
 
 pytestmark = pytest.mark.gpu
 
@@ -64,8 +64,8 @@ def test_decode_through_c_abi(gpu_ops, dtype, num_splits):
     st = lib.kl_paged_decode_attention(*args, workspace.data_ptr(), ws.value, stream_handle())
     assert st == 0, _native.last_error()
     torch.cuda.synchronize()
-    want = ref.paged_decode_attention(q.cpu(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table.cpu(), kv.seq_lens.cpu())
-    torch.testing.assert_close(out.cpu(), want, **tolerance(dtype))
+    want = ref.paged_decode_attention(q.cpu().float(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table.cpu(), kv.seq_lens.cpu())
+    decode_parity(out.cpu(), want, dtype)
 
 
 def test_ops_work_under_torch_compile(gpu_ops):
@@ -89,13 +89,13 @@ def test_ops_work_under_torch_compile(gpu_ops):
         torch.ops.kernel_lab.paged_decode_attention(out, q, k, v, bt, lens, 0.125)
         y = torch.empty_like(x)
         torch.ops.kernel_lab.fused_add_rmsnorm(y, x, r, w, 1e-6)
-        return out + 1, y, r
+        return out * 2, y, r  # doubling is exact, so the check can undo it
 
     r = torch.randn(4, 256, device="cuda", dtype=torch.float16)
     r0 = r.clone()
     out, y, r_new = g(q, kv.k_cache, kv.v_cache, kv.block_table, kv.seq_lens, x, r, w)
-    want = ref.paged_decode_attention(q.cpu(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table.cpu(), kv.seq_lens.cpu(), 0.125)
-    torch.testing.assert_close((out - 1).cpu(), want, **tolerance(torch.float16))
+    want = ref.paged_decode_attention(q.cpu().float(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table.cpu(), kv.seq_lens.cpu(), 0.125)
+    decode_parity((out / 2).cpu(), want, torch.float16, "under torch.compile")
     ref_y, ref_r = ref.fused_add_rms_norm(x.cpu(), r0.cpu(), w.cpu())
     assert torch.equal(r_new.cpu(), ref_r)
     torch.testing.assert_close(y.cpu(), ref_y, **tolerance(torch.float16))
@@ -134,5 +134,5 @@ def test_balanced_request_reaches_the_planner_on_full_batches(gpu_ops, monkeypat
     workspace = torch.empty(sizes[-1][1], dtype=torch.uint8, device="cuda")
     assert lib.kl_paged_decode_attention(*args, workspace.data_ptr(), sizes[-1][1], stream_handle()) == 0
     torch.cuda.synchronize()
-    want = ref.paged_decode_attention(q.cpu(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table.cpu(), kv.seq_lens.cpu())
-    torch.testing.assert_close(out.cpu(), want, **tolerance(torch.float16))
+    want = ref.paged_decode_attention(q.cpu().float(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table.cpu(), kv.seq_lens.cpu())
+    decode_parity(out.cpu(), want, torch.float16)

@@ -16,7 +16,7 @@ import torch
 from kernel_lab import _native
 from kernel_lab.kv_cache import random_cascade_problem
 from oracle import reference as ref
-from tests.conftest import tolerance
+from tests.conftest import decode_parity, tolerance
 
 pytestmark = pytest.mark.gpu
 
@@ -29,7 +29,7 @@ def run(ops, q, c, **kw):
 
 def expected(q, c, scale=None):
     return ref.cascade_decode_attention(
-        q.cpu(), c.kv.k_cache.cpu(), c.kv.v_cache.cpu(), c.prefix_block_table.cpu(), c.prefix_len,
+        q.cpu().float(), c.kv.k_cache.cpu(), c.kv.v_cache.cpu(), c.prefix_block_table.cpu(), c.prefix_len,
         c.kv.block_table.cpu(), c.kv.seq_lens.cpu(), scale,
     )
 
@@ -37,7 +37,7 @@ def expected(q, c, scale=None):
 def check(got, want, dtype):
     got = got.cpu()
     assert torch.isfinite(got).all(), "non-finite output: a NaN page or tail leaked in"
-    torch.testing.assert_close(got, want, **tolerance(dtype))
+    decode_parity(got, want, dtype)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])

@@ -19,7 +19,7 @@ import torch
 
 from kernel_lab.kv_cache import build_paged_kv, device_decode_problem, random_decode_problem
 from oracle import reference as ref
-from tests.conftest import DTYPES, tolerance
+from tests.conftest import DTYPES, decode_parity
 
 pytestmark = pytest.mark.gpu
 
@@ -31,15 +31,17 @@ def run(ops, q, kv, **kw):
 
 
 def expected(q, kv, scale=None):
+    """The oracle's float32 result before its final rounding to q's dtype
+    (q widened exactly; the caches are widened per sequence by the oracle)."""
     return ref.paged_decode_attention(
-        q.cpu(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table.cpu(), kv.seq_lens.cpu(), scale
+        q.cpu().float(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table.cpu(), kv.seq_lens.cpu(), scale
     )
 
 
-def check(got, want, dtype):
-    got = got.cpu()
-    assert torch.isfinite(got).all(), "non-finite output: a poisoned page or tail leaked in"
-    torch.testing.assert_close(got, want, **tolerance(dtype))
+def check(got, want, dtype, what=""):
+    """The reference's tolerance table against the rounded oracle, and at most
+    one output ulp (plus 1e-6) from the unrounded one."""
+    return decode_parity(got, want, dtype, what)
 
 
 # ---------------------------------------------------- original test shapes
@@ -69,17 +71,13 @@ def test_split_kernel_shapes(gpu_ops, hq, hkv, dtype):
 def test_split_kv_is_exact_for_any_split_count(gpu_ops, num_splits, dtype):
     """Splits only partition the sum; empty splits get zero weight (tests/test_paged_attention.py:32-37)."""
     q, kv, _, _ = random_decode_problem([1, 15, 16, 17, 33, 70], 4, 2, 32, 16, dtype=dtype, device="cuda")
-    got = run(gpu_ops, q, kv, num_splits=num_splits)
-    if dtype == torch.float32:
-        torch.testing.assert_close(got.cpu(), expected(q, kv), atol=1e-5, rtol=1e-5)
-    else:
-        check(got, expected(q, kv), dtype)
+    check(run(gpu_ops, q, kv, num_splits=num_splits), expected(q, kv), dtype, f"splits={num_splits}")
 
 
 def test_agrees_with_dense_sdpa(gpu_ops):
     q, kv, keys, values = random_decode_problem([5, 40], 8, 2, 64, 16, dtype=torch.float32, device="cuda")
     want = ref.dense_decode_attention(q.cpu(), [k.cpu() for k in keys], [v.cpu() for v in values])
-    torch.testing.assert_close(run(gpu_ops, q, kv).cpu(), want, atol=1e-5, rtol=1e-5)
+    check(run(gpu_ops, q, kv), want, torch.float32, "dense SDPA")
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -87,11 +85,7 @@ def test_agrees_with_dense_sdpa(gpu_ops):
 @pytest.mark.parametrize("head_dim", [32, 64])
 def test_page_and_head_sizes(gpu_ops, page_size, head_dim, dtype):
     q, kv, _, _ = random_decode_problem([3, 50], 4, 2, head_dim, page_size, dtype=dtype, device="cuda")
-    got = run(gpu_ops, q, kv)
-    if dtype == torch.float32:
-        torch.testing.assert_close(got.cpu(), expected(q, kv), atol=1e-5, rtol=1e-5)
-    else:
-        check(got, expected(q, kv), dtype)
+    check(run(gpu_ops, q, kv), expected(q, kv), dtype)
 
 
 @pytest.mark.parametrize("page_size", [1, 8, 64])
@@ -124,8 +118,8 @@ def test_nan_tails_under_mfma_tiles(gpu_ops, dtype):
 def test_max_seq_len_bounds_work_without_changing_results(gpu_ops):
     q, kv, _, _ = random_decode_problem([5, 20], 4, 2, 32, 16, dtype=torch.float32, device="cuda")
     kv.block_table = torch.nn.functional.pad(kv.block_table, (0, 6))  # extra block-table columns
-    torch.testing.assert_close(run(gpu_ops, q, kv, max_seq_len=20).cpu(), expected(q, kv), atol=1e-5, rtol=1e-5)
-    torch.testing.assert_close(run(gpu_ops, q, kv).cpu(), expected(q, kv), atol=1e-5, rtol=1e-5)
+    check(run(gpu_ops, q, kv, max_seq_len=20), expected(q, kv), torch.float32, "max_seq_len=20")
+    check(run(gpu_ops, q, kv), expected(q, kv), torch.float32)
 
 
 def test_strided_block_table(gpu_ops):
@@ -193,9 +187,8 @@ def test_golden_vectors(gpu_ops, dtype):
         bt = torch.from_numpy(g["block_table"]).cuda()
         lens = torch.from_numpy(g["seq_lens"]).cuda()
         out = gpu_ops.paged_decode_attention(q, k, v, bt, lens, float(g["scale"]))
-        want = torch.from_numpy(data[f"{name}/expected"]).float()
-        tol = {"atol": 1e-5, "rtol": 1e-5} if dtype == torch.float32 else tolerance(dtype)
-        torch.testing.assert_close(out.cpu().float(), want, **tol, msg=lambda m, n=name: f"{n}: {m}")
+        # Expected values are the float64 brute force, unrounded.
+        check(out, torch.from_numpy(data[f"{name}/expected"]), dtype, name)
 
 
 def test_long_context(gpu_ops):
@@ -214,7 +207,7 @@ def test_config2_llama3_gqa(gpu_ops, batch, ctx):
     q, kv = device_decode_problem([ctx] * batch, 32, 8, 128, 16, dtype=torch.float16, seed=batch + ctx)
     want = expected(q, kv)
     for splits in (None, 1, 4, 16, 64):
-        check(run(gpu_ops, q, kv, num_splits=splits), want, torch.float16)
+        check(run(gpu_ops, q, kv, num_splits=splits), want, torch.float16, f"B={batch} ctx={ctx} splits={splits}")
 
 
 def test_config3_ragged_mqa(gpu_ops):
@@ -225,21 +218,13 @@ def test_config3_ragged_mqa(gpu_ops):
     q, kv = device_decode_problem(lens, 32, 1, 128, 16, dtype=torch.bfloat16, seed=3)
     want = expected(q, kv)
     for splits in (None, 1, 7, 64):
-        check(run(gpu_ops, q, kv, num_splits=splits), want, torch.bfloat16)
+        check(run(gpu_ops, q, kv, num_splits=splits), want, torch.bfloat16, f"ragged MQA splits={splits}")
 
 
 def test_config4_long_context_gqa(gpu_ops):
     """64/8/128/16 bf16, B 8, ctx 32768; the planner picks the splits."""
     q, kv = device_decode_problem([32768] * 8, 64, 8, 128, 16, dtype=torch.bfloat16, seed=4)
-    got = run(gpu_ops, q, kv)
-    want = expected(q, kv)
-    check(got, want, torch.bfloat16)
-    # Against the unrounded fp32 result as well: at most one bf16 ulp-ish error.
-    want32 = ref.paged_decode_attention(
-        q.cpu().float(), kv.k_cache.cpu().float(), kv.v_cache.cpu().float(), kv.block_table.cpu(), kv.seq_lens.cpu()
-    )
-    err = (got.cpu().float() - want32).abs().max().item()
-    assert err < 1.6e-2, err
+    check(run(gpu_ops, q, kv), expected(q, kv), torch.bfloat16, "ctx 32768")
 
 
 def test_config4_131072_context(gpu_ops):
@@ -255,9 +240,9 @@ def test_config4_131072_context(gpu_ops):
     assert torch.isfinite(got).all()
     rows = [0, 7]
     want = ref.paged_decode_attention(
-        q[rows].cpu(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table[rows].cpu(), kv.seq_lens[rows].cpu()
+        q[rows].cpu().float(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table[rows].cpu(), kv.seq_lens[rows].cpu()
     )
-    check(got[rows], want, torch.bfloat16)
+    check(got[rows], want, torch.bfloat16, "ctx 131072")
     kv.v_cache.mul_(2)  # NaN spares stay NaN; N(0,1) values stay far from overflow
     doubled = run(gpu_ops, q, kv)
     assert torch.equal(doubled, got * 2), "output is not exactly linear in V"
@@ -300,9 +285,10 @@ def test_balanced_schedule_with_empty_sequences(gpu_ops):
 def test_planner_and_uniform_splits_agree(gpu_ops):
     """The balanced schedule and uniform splits partition the same sum."""
     q, kv, _, _ = random_decode_problem([5000, 3, 700], 32, 8, 128, 16, dtype=torch.float32, device="cuda")
-    a = run(gpu_ops, q.half(), type(kv)(kv.k_cache.half(), kv.v_cache.half(), kv.block_table, kv.seq_lens, 16))
-    b = run(gpu_ops, q.half(), type(kv)(kv.k_cache.half(), kv.v_cache.half(), kv.block_table, kv.seq_lens, 16), num_splits=7)
-    torch.testing.assert_close(a.float().cpu(), b.float().cpu(), atol=2e-3, rtol=2e-3)
+    kv16 = type(kv)(kv.k_cache.half(), kv.v_cache.half(), kv.block_table, kv.seq_lens, 16)
+    want = expected(q.half(), kv16)
+    check(run(gpu_ops, q.half(), kv16), want, torch.float16, "planner")
+    check(run(gpu_ops, q.half(), kv16, num_splits=7), want, torch.float16, "7 splits")
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])

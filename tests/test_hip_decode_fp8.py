@@ -17,7 +17,7 @@ import torch
 from kernel_lab import _native
 from kernel_lab.kv_cache import device_decode_problem, quantize_fp8, random_decode_problem
 from oracle import reference as ref
-from tests.conftest import tolerance
+from tests.conftest import decode_parity, tolerance
 
 pytestmark = pytest.mark.gpu
 
@@ -38,14 +38,14 @@ def run(ops, q, kv, ks, vs, **kw):
 
 def expected(q, kv, ks, vs, scale=None):
     return ref.paged_decode_attention_fp8(
-        q.cpu(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table.cpu(), kv.seq_lens.cpu(), ks.cpu(), vs.cpu(), scale
+        q.cpu().float(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table.cpu(), kv.seq_lens.cpu(), ks.cpu(), vs.cpu(), scale
     )
 
 
 def check(got, want, dtype):
     got = got.cpu()
     assert torch.isfinite(got).all(), "non-finite output: a NaN spare page or tail leaked in"
-    torch.testing.assert_close(got, want, **tolerance(dtype))
+    decode_parity(got, want, dtype)
 
 
 @pytest.mark.parametrize("dtype", QDTYPES)

@@ -22,7 +22,7 @@ import torch
 
 from kernel_lab.kv_cache import device_decode_problem, quantize_fp8, random_decode_problem
 from oracle import reference as ref
-from tests.conftest import tolerance
+from tests.conftest import decode_parity
 
 pytestmark = pytest.mark.gpu
 
@@ -89,9 +89,9 @@ def test_fused_merge_is_bit_identical(gpu_ops, spec, hq, hkv, head_dim, dtype, n
         assert not fused[b].any(), "an empty sequence must give zeros"
     rows = [b for b in range(len(lens)) if b not in empty][:6]
     want = ref.paged_decode_attention(
-        q[rows].cpu(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table[rows].cpu(), kv.seq_lens[rows].cpu()
+        q[rows].cpu().float(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table[rows].cpu(), kv.seq_lens[rows].cpu()
     )
-    torch.testing.assert_close(fused[rows], want, **tolerance(dtype))
+    decode_parity(fused[rows], want, dtype)
 
 
 def test_fused_merge_fp8_cache(gpu_ops):
@@ -103,9 +103,9 @@ def test_fused_merge_fp8_cache(gpu_ops):
     fused = run().cpu()
     assert torch.equal(fused, _unfused(run).cpu())
     want = ref.paged_decode_attention_fp8(
-        q.cpu(), kv8.k_cache.cpu(), kv8.v_cache.cpu(), kv.block_table.cpu(), kv.seq_lens.cpu(), ks.cpu(), vs.cpu()
+        q.cpu().float(), kv8.k_cache.cpu(), kv8.v_cache.cpu(), kv.block_table.cpu(), kv.seq_lens.cpu(), ks.cpu(), vs.cpu()
     )
-    torch.testing.assert_close(fused, want, **tolerance(torch.bfloat16))
+    decode_parity(fused, want, torch.bfloat16)
 
 
 def test_counters_are_left_at_zero(gpu_ops):
@@ -188,9 +188,9 @@ def test_empty_sequences_beyond_the_grid(gpu_ops, batch, hq, hkv, max_len, split
     assert torch.equal(fused, merged)
     rows = [0, 2, batch // 2, batch - 2]
     want = ref.paged_decode_attention(
-        q[rows].cpu(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table[rows].cpu(), kv.seq_lens[rows].cpu()
+        q[rows].cpu().float(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table[rows].cpu(), kv.seq_lens[rows].cpu()
     )
-    torch.testing.assert_close(fused[rows], want, **tolerance(torch.float16))
+    decode_parity(fused[rows], want, torch.float16)
 
 
 @pytest.mark.parametrize(("lens", "splits"), [([4096] * 8, None), ([900] * 16, 6), ([30000, 40, 500], None)])

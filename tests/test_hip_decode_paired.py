@@ -30,7 +30,7 @@ import torch
 
 from kernel_lab.kv_cache import device_decode_problem, quantize_fp8, random_decode_problem
 from oracle import reference as ref
-from tests.conftest import tolerance
+from tests.conftest import decode_parity
 
 pytestmark = pytest.mark.gpu
 
@@ -83,9 +83,9 @@ def test_paired_matches_unpaired_and_oracle(gpu_ops, batch, hq, hkv, head_dim, d
     assert torch.isfinite(paired).all(), "non-finite output: a poisoned page or tail leaked in"
     assert torch.equal(paired, single), "paired workgroups changed the result"
     want = ref.paged_decode_attention(
-        q.cpu(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table.cpu(), kv.seq_lens.cpu()
+        q.cpu().float(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table.cpu(), kv.seq_lens.cpu()
     )
-    torch.testing.assert_close(paired, want, **tolerance(dtype))
+    decode_parity(paired, want, dtype)
     for b in empties:
         assert not paired[b].any(), "an empty sequence must give zeros"
 
@@ -108,9 +108,9 @@ def test_paired_fp8_cache_matches_unpaired(gpu_ops):
             os.environ["KL_DECODE_PAIRED"] = old
     assert torch.equal(paired.cpu(), single.cpu()), "paired workgroups changed the FP8 result"
     want = ref.paged_decode_attention_fp8(
-        q.cpu(), k8.cpu(), v8.cpu(), kv.block_table.cpu(), kv.seq_lens.cpu(), ks.cpu(), vs.cpu()
+        q.cpu().float(), k8.cpu(), v8.cpu(), kv.block_table.cpu(), kv.seq_lens.cpu(), ks.cpu(), vs.cpu()
     )
-    torch.testing.assert_close(paired.cpu(), want, **tolerance(torch.float16))
+    decode_parity(paired.cpu(), want, torch.float16)
 
 
 # The balanced schedule: the planner's choice below 256 units, or requested
@@ -156,11 +156,11 @@ def test_balanced_schedule_pairing(gpu_ops, spec, hq, hkv, head_dim, dtype, num_
         assert torch.equal(got, single), "the pairing switch changed the single-head balanced schedule"
     rows = [b for b in range(len(lens)) if b not in empties][:8]
     want = ref.paged_decode_attention(
-        q[rows].cpu(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table[rows].cpu(), kv.seq_lens[rows].cpu()
+        q[rows].cpu().float(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table[rows].cpu(), kv.seq_lens[rows].cpu()
     )
     for out in (got, single):
         assert torch.isfinite(out).all(), "non-finite output: a poisoned page or tail leaked in"
-        torch.testing.assert_close(out[rows], want, **tolerance(dtype))
+        decode_parity(out[rows], want, dtype)
         for b in empties:
             assert not out[b].any(), "an empty sequence must give zeros"
 
@@ -196,9 +196,9 @@ def test_long_context_pairs_equal_uniform_splits(gpu_ops, batch, ctx, splits, dt
     assert torch.equal(planned, uniform)
     rows = [0, batch - 1]
     want = ref.paged_decode_attention(
-        q[rows].cpu(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table[rows].cpu(), kv.seq_lens[rows].cpu()
+        q[rows].cpu().float(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table[rows].cpu(), kv.seq_lens[rows].cpu()
     )
-    torch.testing.assert_close(planned[rows].cpu(), want, **tolerance(dtype))
+    decode_parity(planned[rows].cpu(), want, dtype)
 
 
 @pytest.mark.parametrize(
@@ -221,10 +221,10 @@ def test_long_context_pairs_other_pages_and_head_dims(gpu_ops, lens_spec, head_d
     got, single = _both(gpu_ops, q, kv)
     rows = [b for b in range(len(lens)) if b not in empty][:3]
     want = ref.paged_decode_attention(
-        q[rows].cpu(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table[rows].cpu(), kv.seq_lens[rows].cpu()
+        q[rows].cpu().float(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table[rows].cpu(), kv.seq_lens[rows].cpu()
     )
     for out in (got, single):
         assert torch.isfinite(out).all()
-        torch.testing.assert_close(out[rows], want, **tolerance(dtype))
+        decode_parity(out[rows], want, dtype)
         for b in empty:
             assert not out[b].any(), "an empty sequence must give zeros"

@@ -14,7 +14,7 @@ import torch
 
 from kernel_lab.kv_cache import random_decode_problem
 from oracle import reference as ref
-from tests.conftest import tolerance
+from tests.conftest import decode_parity
 
 pytestmark = pytest.mark.gpu
 
@@ -51,10 +51,10 @@ def test_random_decode_case(gpu_ops, seed):
     if empty:
         kv.seq_lens[0] = 0
     got = gpu_ops.paged_decode_attention(q, kv.k_cache, kv.v_cache, kv.block_table, kv.seq_lens, num_splits=splits)
-    want = ref.paged_decode_attention(q.cpu(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table.cpu(),
+    want = ref.paged_decode_attention(q.cpu().float(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table.cpu(),
                                       kv.seq_lens.cpu())
     if empty:
         want[0] = 0
     got = got.cpu()
     assert torch.isfinite(got).all(), case
-    torch.testing.assert_close(got, want, **tolerance(dtype), msg=lambda m: f"{case}: {m}")
+    decode_parity(got, want, dtype, case)
