@@ -143,6 +143,30 @@ int kl_paged_decode_attention(kl_dtype dtype, void* out, const void* q, const vo
                               kl_stream_t stream);
 
 /*
+ * kl_paged_decode_attention without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops
+ * that forbid allocation). No counterpart exists in the reference: its
+ * launchers need no split workspace, and its Triton wrapper allocates one per
+ * call (kernel_lab/triton_kernels/paged_attention.py:213-214).
+ *
+ * The split workspace lives in a library-owned 16 MiB device array, one per
+ * device, held until the process ends; it fits every split the planner
+ * chooses by itself (num_splits 0). A plan needing more (explicit split
+ * counts over large batches) returns KL_ERR_WORKSPACE without launching.
+ * The first call on a device looks up that device's array; the call
+ * allocates nothing (no hipMalloc, no hipFree). Calls that overlap on one
+ * device share the array and race: run them on one stream, or use
+ * kl_paged_decode_attention with a workspace per stream. Other arguments,
+ * results and status codes are those of kl_paged_decode_attention.
+ */
+int kl_paged_decode_attention_noalloc(kl_dtype dtype, void* out, const void* q, const void* k_cache,
+                                      const void* v_cache, const int32_t* block_table,
+                                      const int32_t* seq_lens, int batch, int num_q_heads,
+                                      int num_kv_heads, int head_dim, int page_size,
+                                      int64_t block_table_stride, int max_pages, float scale,
+                                      int num_splits, kl_stream_t stream);
+
+/*
  * Paged decode over an FP8 KV cache: k_cache / v_cache hold OCP FP8 E4M3
  * codes ("e4m3fn": bias 7, no infinities, 0x7f / 0xff are NaN), one byte per
  * element, in the same [num_pages, page_size, num_kv_heads, head_dim] layout;

@@ -48,6 +48,7 @@
 // token; each lane keeps an online softmax per query head and lanes merge by
 // the log-sum-exp rule at the end.
 #include <algorithm>
+#include <cstdio>
 #include <cstdlib>
 #include <cmath>
 #include <mutex>
@@ -2191,6 +2192,88 @@ extern "C" int kl_paged_decode_attention(kl_dtype dtype, void* out, const void* 
   return kl::decode_entry(dtype, false, out, q, k_cache, v_cache, nullptr, nullptr, block_table, seq_lens, batch,
                           num_q_heads, num_kv_heads, head_dim, page_size, block_table_stride, max_pages, scale,
                           num_splits, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+}
+
+// --------------------------------------------- no-allocation decode entry point
+//
+// The split workspace of kl_paged_decode_attention (fp32 partial outputs and
+// their log2-sum-exps) for callers that cannot allocate device memory, in a
+// library-owned array. 16 MiB holds every split the planner chooses by itself
+// (num_splits 0): at most about 8.5 MB, 511 balanced slots of 32 heads x 129
+// floats or 16 heads x 257. Each device holds its own copy until the process
+// ends. No byte of it has to start at zero: a merge reads only partials that
+// the same call wrote before. Calls that overlap on one device share it, so
+// they race.
+constexpr size_t kScratchBytes = size_t{16} << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace kl {
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+
+// Device address of the current device's `scratch`. Host code never uses the
+// array's own name as an address (it is a host-side stand-in): the runtime
+// reports each device's copy once, with that device current, and the address
+// is kept per device. Null (with the error recorded) if the lookup fails.
+void* scratch_for_current_device() {
+  static std::mutex mu;
+  static void* addr[kMaxScratchDevices] = {};
+  int dev = 0;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    fail_hip(e, "hipGetDevice");
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxScratchDevices) {
+    fail(KL_ERR_UNSUPPORTED, "device index beyond the no-allocation entry point's table");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (addr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess) {
+      fail_hip(err, "hipGetSymbolAddress(scratch)");
+      return nullptr;
+    }
+    addr[dev] = p;
+  }
+  return addr[dev];
+}
+
+}  // namespace
+}  // namespace kl
+
+extern "C" int kl_paged_decode_attention_noalloc(kl_dtype dtype, void* out, const void* q, const void* k_cache,
+                                                 const void* v_cache, const int32_t* block_table,
+                                                 const int32_t* seq_lens, int batch, int num_q_heads,
+                                                 int num_kv_heads, int head_dim, int page_size,
+                                                 int64_t block_table_stride, int max_pages, float scale,
+                                                 int num_splits, kl_stream_t stream) {
+  using namespace kl;
+  // Set-up first: the device's scratch address is looked up on the first call
+  // on each device, whatever this call needs.
+  void* ws = scratch_for_current_device();
+  if (ws == nullptr) return KL_ERR_HIP;
+  if (batch == 0) return ok();
+  int splits = 0;
+  size_t need = 0;
+  const int st = kl_paged_decode_plan(dtype, batch, num_q_heads, num_kv_heads, head_dim, page_size, max_pages,
+                                      num_splits, 0, &splits, &need);
+  if (st != KL_OK) return st;
+  if (need > kScratchBytes) {
+    char msg[200];
+    std::snprintf(msg, sizeof(msg),
+                  "this split plan needs %zu bytes of workspace; the no-allocation entry point holds %zu "
+                  "(use kl_paged_decode_attention with a caller workspace, or fewer splits)",
+                  need, kScratchBytes);
+    return fail(KL_ERR_WORKSPACE, msg);
+  }
+  return kl::decode_entry(dtype, false, out, q, k_cache, v_cache, nullptr, nullptr, block_table, seq_lens, batch,
+                          num_q_heads, num_kv_heads, head_dim, page_size, block_table_stride, max_pages, scale,
+                          num_splits, need > 0 ? ws : nullptr, need > 0 ? kScratchBytes : 0,
+                          reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int kl_paged_decode_attention_fp8(kl_dtype dtype, void* out, const void* q, const void* k_cache,

@@ -196,3 +196,25 @@ def test_one_hip_runtime_in_process():
     maps = Path("/proc/self/maps").read_text()
     paths = {line.split()[-1] for line in maps.splitlines() if "libamdhip64" in line}
     assert len(paths) <= 1, paths
+
+
+def test_planner_choices_fit_the_no_allocation_array():
+    """kl_paged_decode_attention_noalloc holds 16 MiB of split workspace per
+    device; every plan the planner makes by itself (num_splits 0) on MI355X's
+    256 CUs must fit it, across batch sizes, GQA layouts, head dims, context
+    widths and dtypes."""
+    lib = _native.core()
+    splits, ws = ctypes.c_int(0), ctypes.c_size_t(0)
+    worst = (0, None)
+    for code in (0, 1, 2):
+        for batch in (1, 2, 3, 7, 8, 16, 31, 32, 33, 63, 64, 100, 127, 128, 255, 256, 257, 511, 512, 1024):
+            for hq, hkv in ((32, 8), (32, 1), (64, 8), (8, 1), (16, 16), (40, 5), (64, 2), (128, 8), (64, 1), (96, 4)):
+                for d in (32, 64, 128, 256):
+                    for max_pages in (1, 32, 256, 2048, 8192):
+                        st = lib.kl_paged_decode_plan(code, batch, hq, hkv, d, 16, max_pages, 0, 256,
+                                                      ctypes.byref(splits), ctypes.byref(ws))
+                        if st != 0:
+                            continue  # shapes the dtype has no kernel for (fp32 head_dim 256 x 64 lanes ...)
+                        if ws.value > worst[0]:
+                            worst = (ws.value, (code, batch, hq, hkv, d, max_pages))
+    assert 0 < worst[0] <= 16 << 20, worst
