@@ -36,6 +36,11 @@ typedef enum kl_dtype {
 /* num_splits value asking paged decode for the device-balanced schedule. */
 #define KL_SPLITS_BALANCED (-1)
 
+/* kl_paged_decode_last_merge results. */
+#define KL_MERGE_NONE 0      /* no sequence was split (or the call failed)   */
+#define KL_MERGE_KERNEL 1    /* split sequences merged by a second launch    */
+#define KL_MERGE_IN_KERNEL 2 /* merged by the decode kernel's last segment   */
+
 /*
  * Status codes. The reference launchers return cudaError_t and signal
  * unsupported shapes with cudaErrorInvalidValue (csrc/paged_attention.cu:157,
@@ -125,14 +130,15 @@ int kl_paged_decode_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_
  * Split sequences are merged inside the decode kernel where the path allows
  * it (fp16/bf16, at most 8 query heads per KV head and head group, and a
  * sequence cut into few enough segments that one workgroup's merge stays
- * short; otherwise a separate merge launch runs): the
- * library keeps per-device arrival counters (512 KiB) in 16 regions, each
- * taken by the first stream that needs one and reused by that stream's later
- * calls, which the stream runs one after another. A call on a stream beyond
- * the 16 falls back to a separate merge launch; results are bit-identical
- * either way. KL_DECODE_FUSED_MERGE=0 in the environment forces the merge
- * launch. A captured graph keeps the region of the stream it was captured on:
- * replaying it on another stream while that stream runs decode calls races.
+ * short; otherwise a separate merge launch runs). The library keeps
+ * per-device arrival counters (8 MiB) in regions that calls able to overlap
+ * never share: an eager call uses its stream's region (64 streams per
+ * device), a call recorded under graph capture a region of its own capture
+ * sequence and stream (192 per device, never reused), so graphs may replay
+ * concurrently on any streams. hipStreamPerThread, and streams or captures
+ * beyond those counts (reported once on stderr), use the merge launch;
+ * results are bit-identical either way. KL_DECODE_FUSED_MERGE=0 in the
+ * environment forces the merge launch.
  */
 int kl_paged_decode_attention(kl_dtype dtype, void* out, const void* q, const void* k_cache,
                               const void* v_cache, const int32_t* block_table,
@@ -141,6 +147,15 @@ int kl_paged_decode_attention(kl_dtype dtype, void* out, const void* q, const vo
                               int64_t block_table_stride, int max_pages, float scale,
                               int num_splits, void* workspace, size_t workspace_bytes,
                               kl_stream_t stream);
+
+/*
+ * How the last paged-decode call on the calling thread (any of the
+ * kl_paged_decode_attention entry points) combined split sequences: one of
+ * KL_MERGE_NONE, KL_MERGE_KERNEL, KL_MERGE_IN_KERNEL. A diagnostic for
+ * performance work and tests; no counterpart in the reference, whose
+ * launchers do not split sequences.
+ */
+int kl_paged_decode_last_merge(void);
 
 /*
  * kl_paged_decode_attention without a workspace argument, for callers that

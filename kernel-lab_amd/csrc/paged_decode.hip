@@ -666,12 +666,19 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
 // missing arrival cannot hang a workgroup.
 //
 // The counters live in device memory owned by the library, zero when the
-// code object is loaded and zero again after every call. A call takes the
-// counters of a region that belongs to its stream (kernels on one stream
-// never overlap); with more streams than regions the call falls back to the
-// merge kernel.
-constexpr int kArrivalRegions = 16;      // streams served per device
-constexpr int kArrivalCounters = 8192;   // units per region
+// code object is loaded and zero again after every completed call (the last
+// arriver of each unit resets its counter). Calls whose kernels may overlap
+// must not share counters, so a call takes a region that only calls ordered
+// with it use (arrival_region): an eager call the region of its stream
+// (kernels on one stream never overlap), a call recorded into a graph a
+// region of its own capture sequence and capture stream, never shared with
+// eager streams or other captures. With the regions of a kind used up, or on
+// a per-thread default stream (one handle, many streams), the call takes the
+// merge kernel; results are bit-identical either way.
+constexpr int kStreamRegions = 64;       // eager streams served per device
+constexpr int kCaptureRegions = 192;     // captured (capture sequence, stream) pairs per device
+constexpr int kArrivalRegions = kStreamRegions + kCaptureRegions;
+constexpr int kArrivalCounters = 8192;   // units per region (8 MiB per device in all)
 // Query heads of a fused unit (one head tile, at most two heads per wave).
 // Measured on MI355X for MQA units (32 heads, two head tiles): the last
 // arriver's 8-heads-per-wave merge made the ragged 64-sequence batch slower
@@ -1731,23 +1738,51 @@ bool fused_merge_enabled() {
   return v == nullptr || v[0] != '0';
 }
 
-// The arrival-counter region of `stream` on the current device (taken on the
-// stream's first fused call and kept: a stream's kernels run one after
-// another, so its calls can share one region), or null when every region of
-// the device belongs to other streams or the counters cannot be located.
+// The arrival-counter region for a fused call on `stream` (current device),
+// or null for the merge kernel.
+//   eager stream      the stream's own region, taken on its first fused call
+//                     and kept (its calls run one after another);
+//   capturing stream  a region of its own for each (capture sequence, capture
+//                     stream): every launch of the resulting graph node
+//                     replays with it, and a graph never runs concurrently
+//                     with itself, while two graphs, or a graph and eager
+//                     work, may; regions of captures are never reused (the
+//                     library cannot see a graph's destruction);
+//   hipStreamPerThread, a broken capture, or an unreadable stream: none.
+// A pool that runs out is reported once per device on stderr.
 uint32_t* arrival_region(hipStream_t stream) {
+  if (stream == hipStreamPerThread) return nullptr;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  unsigned long long capture = 0;
+  if (hipStreamGetCaptureInfo(stream, &cs, &capture) != hipSuccess) {
+    (void)hipGetLastError();  // the launch check must not see this error
+    return nullptr;
+  }
+  if (cs == hipStreamCaptureStatusInvalidated) return nullptr;
+  const bool capturing = cs == hipStreamCaptureStatusActive;
+  struct Owner {
+    hipStream_t stream;
+    unsigned long long capture;  // 0: eager
+  };
   struct Device {
     uint32_t* base = nullptr;
     bool located = false;
-    hipStream_t owner[kArrivalRegions] = {};
-    int taken = 0;
+    Owner eager[kStreamRegions] = {};
+    Owner captured[kCaptureRegions] = {};
+    int eager_taken = 0;
+    int captured_taken = 0;
+    bool warned_eager = false;
+    bool warned_captured = false;
   };
+  constexpr int kMaxDevices = 64;
   static std::mutex mu;
-  static std::vector<Device> devices;
+  static Device devices[kMaxDevices];
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return nullptr;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
   std::lock_guard<std::mutex> lock(mu);
-  if (static_cast<size_t>(dev) >= devices.size()) devices.resize(dev + 1);
   Device& d = devices[dev];
   if (!d.located) {
     d.located = true;
@@ -1761,13 +1796,34 @@ uint32_t* arrival_region(hipStream_t stream) {
     }
   }
   if (d.base == nullptr) return nullptr;
-  for (int i = 0; i < d.taken; ++i) {
-    if (d.owner[i] == stream) return d.base + static_cast<size_t>(i) * kArrivalCounters;
+  Owner* pool = capturing ? d.captured : d.eager;
+  int& taken = capturing ? d.captured_taken : d.eager_taken;
+  const int size = capturing ? kCaptureRegions : kStreamRegions;
+  const int first = capturing ? kStreamRegions : 0;  // region index of the pool's first entry
+  const unsigned long long key = capturing ? capture : 0;
+  for (int i = 0; i < taken; ++i) {
+    if (pool[i].stream == stream && pool[i].capture == key) {
+      return d.base + static_cast<size_t>(first + i) * kArrivalCounters;
+    }
   }
-  if (d.taken == kArrivalRegions) return nullptr;
-  d.owner[d.taken] = stream;
-  return d.base + static_cast<size_t>(d.taken++) * kArrivalCounters;
+  if (taken == size) {
+    bool& warned = capturing ? d.warned_captured : d.warned_eager;
+    if (!warned) {
+      warned = true;
+      std::fprintf(stderr,
+                   "kernel_lab: device %d: all %d split-merge counter regions for %s are taken; further split "
+                   "decode calls there use the separate merge kernel (same results, a few microseconds slower)\n",
+                   dev, size, capturing ? "graph captures" : "streams");
+    }
+    return nullptr;
+  }
+  pool[taken] = Owner{stream, key};
+  return d.base + static_cast<size_t>(first + taken++) * kArrivalCounters;
 }
+
+// How the last decode launch on this thread combined split units
+// (kl_paged_decode_last_merge).
+thread_local int g_last_merge = KL_MERGE_NONE;
 
 // Arrival counters for a split decode of `units` units with up to
 // heads_per_wg heads each on the MFMA path, or null for the merge kernel.
@@ -2034,7 +2090,9 @@ int launch_balanced(DecodeArgs a, int head_dim, hipStream_t stream) {
   });
   if (st != KL_OK) return st;
   st = check_launch("paged decode balanced kernel launch");
-  if (st != KL_OK || a.arrivals != nullptr) return st;
+  if (st != KL_OK) return st;
+  g_last_merge = a.arrivals != nullptr ? KL_MERGE_IN_KERNEL : KL_MERGE_KERNEL;
+  if (a.arrivals != nullptr) return st;
   decode_merge_balanced_kernel<E>
       <<<static_cast<unsigned>(static_cast<int64_t>(a.batch) * a.num_q_heads), 64, 0, stream>>>(a, head_dim);
   return check_launch("paged decode balanced merge kernel launch");
@@ -2064,6 +2122,7 @@ int launch_typed(DecodeArgs& a, int head_dim, bool mfma, hipStream_t stream) {
   if (st != KL_OK) return st;
   st = check_launch("paged decode split kernel launch");
   if (st != KL_OK) return st;
+  g_last_merge = a.num_splits <= 1 ? KL_MERGE_NONE : a.arrivals != nullptr ? KL_MERGE_IN_KERNEL : KL_MERGE_KERNEL;
   if (a.num_splits > 1 && a.arrivals == nullptr) {
     decode_merge_kernel<E><<<static_cast<unsigned>(static_cast<int64_t>(a.batch) * a.num_q_heads), 64, 0, stream>>>(
         a, head_dim);
@@ -2099,6 +2158,7 @@ int decode_entry(kl_dtype dtype, bool kv8, void* out, const void* q, const void*
                  int batch, int num_q_heads, int num_kv_heads, int head_dim, int page_size,
                  int64_t block_table_stride, int max_pages, float scale, int num_splits, void* workspace,
                  size_t workspace_bytes, hipStream_t stream) {
+  g_last_merge = KL_MERGE_NONE;
   if (batch == 0) return ok();
   if (kv8) {
     if (dtype != KL_DTYPE_F16 && dtype != KL_DTYPE_BF16) {
@@ -2193,6 +2253,8 @@ extern "C" int kl_paged_decode_attention(kl_dtype dtype, void* out, const void* 
                           num_q_heads, num_kv_heads, head_dim, page_size, block_table_stride, max_pages, scale,
                           num_splits, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
 }
+
+extern "C" int kl_paged_decode_last_merge(void) { return kl::g_last_merge; }
 
 // --------------------------------------------- no-allocation decode entry point
 //

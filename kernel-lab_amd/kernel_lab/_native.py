@@ -43,6 +43,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _i32,
         [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i64, _i32, _f32, _vp, _sz, _vp],
     ),
+    "kl_paged_decode_last_merge": (_i32, []),
     "kl_paged_decode_attention_noalloc": (
         _i32,
         [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i64, _i32, _f32, _i32, _vp],

@@ -9,8 +9,9 @@ region that belongs to the call's stream. The merge is the merge kernels' own
 routine, so every output must be bit-identical with the fused merge switched
 off (``KL_DECODE_FUSED_MERGE=0``), and match the oracle. The counters must be
 left at zero by every call (back-to-back calls of different shapes), streams
-must not share counters (concurrent streams), and a stream beyond the
-library's 16 regions per device must fall back to the merge kernel.
+must not share counters (concurrent streams), and every case checks, through
+kl_paged_decode_last_merge, that the merge it expects actually ran. Streams
+beyond the library's regions: tests/test_zy_merge_regions.py.
 """
 
 from __future__ import annotations
@@ -20,6 +21,7 @@ import os
 import pytest
 import torch
 
+from kernel_lab import _native
 from kernel_lab.kv_cache import device_decode_problem, quantize_fp8, random_decode_problem
 from oracle import reference as ref
 from tests.conftest import decode_parity
@@ -48,22 +50,29 @@ def _lens(batch: int, hi: int, seed: int) -> list[int]:
     return torch.randint(1, hi + 1, (batch,), generator=g).tolist()
 
 
+IN_KERNEL, MERGE_KERNEL = 2, 1  # kl_paged_decode_last_merge: KL_MERGE_IN_KERNEL, KL_MERGE_KERNEL
+
+
+def _last_merge() -> int:
+    return _native.core().kl_paged_decode_last_merge()
+
+
 CASES = [
-    # (lens, hq, hkv, head_dim, dtype, num_splits, empty rows); None = planner
-    ([512], 32, 8, 128, torch.float16, None, []),  # balanced, B=1
-    ([4096] * 8, 32, 8, 128, torch.float16, None, []),  # balanced, units split 4 ways
-    ([65536] + [1024] * 15, 32, 8, 128, torch.float16, None, []),  # skewed, balanced
-    ("r24", 64, 8, 128, torch.bfloat16, None, [3, 17]),  # G=8, empty sequences
-    ("r64", 32, 8, 128, torch.float16, -1, [0, 63]),  # balanced on request, full batch
-    ([900] * 8, 32, 8, 128, torch.float16, 4, []),  # uniform splits
-    ([1, 15, 16, 17, 33, 70, 300, 1025], 16, 4, 64, torch.bfloat16, 16, [2]),  # splits past short sequences
-    ("r16", 8, 8, 32, torch.float16, 5, []),  # G=1, head_dim 32
-    ([2000] * 64, 32, 8, 128, torch.float16, 2, [5]),  # paired workgroups with splits
-    ("m64", 32, 1, 128, torch.bfloat16, None, [9]),  # MQA: 32-head units (merge kernel), balanced
-    ([6000, 30, 2500, 800], 32, 1, 64, torch.float16, 7, []),  # MQA, uniform splits, head_dim 64
-    ([3000] * 4, 96, 4, 128, torch.float16, None, []),  # 24 heads per unit (two head tiles)
-    ([32768], 8, 1, 128, torch.float16, None, []),  # one unit over 256 workgroups: the merge kernel
-    ([2048], 8, 1, 128, torch.float16, None, []),  # one unit over 16 workgroups: merged in-kernel
+    # (lens, hq, hkv, head_dim, dtype, num_splits, empty rows, merge); None = planner
+    ([512], 32, 8, 128, torch.float16, None, [], IN_KERNEL),  # balanced, B=1
+    ([4096] * 8, 32, 8, 128, torch.float16, None, [], IN_KERNEL),  # balanced, units split 4 ways
+    ([65536] + [1024] * 15, 32, 8, 128, torch.float16, None, [], IN_KERNEL),  # skewed, balanced
+    ("r24", 64, 8, 128, torch.bfloat16, None, [3, 17], IN_KERNEL),  # G=8, empty sequences
+    ("r64", 32, 8, 128, torch.float16, -1, [0, 63], IN_KERNEL),  # balanced on request, full batch
+    ([900] * 8, 32, 8, 128, torch.float16, 4, [], IN_KERNEL),  # uniform splits
+    ([1, 15, 16, 17, 33, 70, 300, 1025], 16, 4, 64, torch.bfloat16, 16, [2], IN_KERNEL),  # splits past short ones
+    ("r16", 8, 8, 32, torch.float16, 5, [], IN_KERNEL),  # G=1, head_dim 32
+    ([2000] * 64, 32, 8, 128, torch.float16, 2, [5], IN_KERNEL),  # paired workgroups with splits
+    ("m64", 32, 1, 128, torch.bfloat16, None, [9], MERGE_KERNEL),  # MQA: 32-head units, balanced
+    ([6000, 30, 2500, 800], 32, 1, 64, torch.float16, 7, [], MERGE_KERNEL),  # MQA, uniform splits, head_dim 64
+    ([3000] * 4, 96, 4, 128, torch.float16, None, [], MERGE_KERNEL),  # 24 heads per unit (two head tiles)
+    ([32768], 8, 1, 128, torch.float16, None, [], MERGE_KERNEL),  # one unit over 256 workgroups
+    ([2048], 8, 1, 128, torch.float16, None, [], IN_KERNEL),  # one unit over 16 workgroups
 ]
 
 
@@ -74,15 +83,17 @@ def _case_lens(spec):
     return list(spec)
 
 
-@pytest.mark.parametrize(("spec", "hq", "hkv", "head_dim", "dtype", "num_splits", "empty"), CASES)
-def test_fused_merge_is_bit_identical(gpu_ops, spec, hq, hkv, head_dim, dtype, num_splits, empty):
+@pytest.mark.parametrize(("spec", "hq", "hkv", "head_dim", "dtype", "num_splits", "empty", "merge"), CASES)
+def test_fused_merge_is_bit_identical(gpu_ops, spec, hq, hkv, head_dim, dtype, num_splits, empty, merge):
     lens = _case_lens(spec)
     q, kv = device_decode_problem(lens, hq, hkv, head_dim, 16, dtype=dtype, seed=len(lens) + hq)
     if empty:
         kv.seq_lens[empty] = 0
     kw = {} if num_splits is None else {"num_splits": num_splits}
     fused = _decode(gpu_ops, q, kv, **kw).cpu()
+    assert _last_merge() == merge, "the call did not take the expected merge"
     merged = _unfused(lambda: _decode(gpu_ops, q, kv, **kw)).cpu()
+    assert _last_merge() == MERGE_KERNEL
     assert torch.isfinite(fused).all(), "non-finite output: a poisoned page or tail leaked in"
     assert torch.equal(fused, merged), "fused merge differs from the merge kernel"
     for b in empty:
@@ -142,24 +153,6 @@ def test_concurrent_streams(gpu_ops):
         torch.cuda.synchronize()
         for _, _, _, out, want in jobs:
             assert torch.equal(out, want)
-
-
-def test_streams_beyond_the_regions_fall_back(gpu_ops):
-    """More streams than counter regions: the extra streams use the merge
-    kernel and still give the same bits."""
-    q, kv = device_decode_problem([1800] * 4, 32, 8, 128, 16, dtype=torch.float16, seed=80)
-    want = _unfused(lambda: _decode(gpu_ops, q, kv)).clone()
-    outs = []
-    for _ in range(24):
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        out = torch.empty_like(q)
-        with torch.cuda.stream(s):
-            _decode(gpu_ops, q, kv, out=out)
-        outs.append(out)
-    torch.cuda.synchronize()
-    for out in outs:
-        assert torch.equal(out, want)
 
 
 @pytest.mark.parametrize(

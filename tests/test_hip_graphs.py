@@ -9,6 +9,7 @@ from __future__ import annotations
 import pytest
 import torch
 
+from kernel_lab import _native
 from kernel_lab.kv_cache import device_decode_problem, quantize_fp8
 
 pytestmark = pytest.mark.gpu
@@ -88,3 +89,41 @@ def test_fp8_and_rmsnorm_graph_replays(gpu_ops):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, want_out) and torch.equal(y, want_y) and torch.equal(res, want_res), i
+
+
+def test_concurrent_replays_of_two_graphs(gpu_ops):
+    """Two decode graphs captured on torch's shared capture stream, replayed
+    at the same time on two streams, twenty times. Each captured call merges
+    its split units inside the decode kernel, on arrival counters of its own
+    capture: graphs that shared counters would count each other's arrivals and
+    merge early (stale partials) or never (the output left as NaN)."""
+    jobs = []
+    for i, lens in enumerate(([4096] * 8, [3000, 17, 2500, 900, 4096, 1, 2048, 300])):
+        q, kv = device_decode_problem(lens, 32, 8, 128, 16, dtype=torch.float16, seed=70 + i)
+        outs = [torch.empty_like(q) for _ in range(4)]
+
+        def run(q=q, kv=kv, outs=outs):
+            for o in outs:
+                gpu_ops.paged_decode_attention(q, kv.k_cache, kv.v_cache, kv.block_table, kv.seq_lens, out=o)
+
+        run()
+        want = [o.clone() for o in outs]
+        g = capture(run)
+        assert _native.core().kl_paged_decode_last_merge() == 2, "captured calls should merge in-kernel"
+        # A graph reads its inputs where they were at capture: they must stay
+        # allocated while it replays (the closure alone does not hold them
+        # once the next iteration rebinds it).
+        jobs.append((g, outs, want, torch.cuda.Stream(), (q, kv)))
+    torch.cuda.synchronize()
+    for rep in range(20):
+        for _, outs, _, _, _ in jobs:
+            for o in outs:
+                o.fill_(float("nan"))
+        for g, _, _, stream, _ in jobs:
+            stream.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(stream):
+                g.replay()
+        torch.cuda.synchronize()
+        for i, (_, outs, want, _, _) in enumerate(jobs):
+            for o, w in zip(outs, want):
+                assert torch.equal(o, w), f"replay {rep} of graph {i} differs from eager"
