@@ -14,8 +14,8 @@
 // is reduced within each wave by DPP, across waves through LDS with one
 // barrier, and the output is written from registers: one read of x and the
 // residual, one write of the residual and the output, nothing re-read.
-// Rows too wide for the register budget use a two-pass variant whose second
-// pass re-reads the row.
+// Rows too wide for the register budget use a two-pass variant that keeps the
+// rounded sum in LDS (and forms it again for what LDS cannot hold).
 #include <algorithm>
 
 #include "hip_common.h"
@@ -154,49 +154,78 @@ __global__ void __launch_bounds__(kMaxThreads)
   }
 }
 
-// Two-pass variant for rows wider than the register-resident kernel takes.
-// Pass 1 writes the residual and reduces; pass 2 re-reads the row the same
-// thread wrote (no cross-thread dependency, so no extra barrier).
+// Rows wider than the register-resident kernel holds (more than 8 packs per
+// thread at 1024 threads: 65,536 16-bit or 32,768 fp32 elements aligned, 8,192
+// unaligned). Two passes over the row with the rounded sum kept in LDS:
+//   pass 1  reads x (and the residual), forms the rounded sum, accumulates its
+//           squares, and keeps the sum of the row's first kStagedPacks packs in
+//           LDS (writing their residual now);
+//   pass 2  normalises from LDS; packs beyond the LDS window are formed again
+//           from x and the residual, whose original value is still in memory
+//           because pass 1 did not write those packs, and their residual is
+//           written then.
+// A thread takes the same packs in both passes, so neither pass waits for
+// another thread beyond the reduction's barrier; the squares are summed in the
+// same order either way, so the bits do not depend on the LDS window.
+constexpr int kStageBytes = 48 * 1024;
+
 template <typename E, int VEC, bool HAS_RES>
 __global__ void __launch_bounds__(kMaxThreads)
-    rms_norm_stream_kernel(typename E::S* __restrict__ out, const typename E::S* __restrict__ x,
+    rms_norm_staged_kernel(typename E::S* __restrict__ out, const typename E::S* __restrict__ x,
                            typename E::S* __restrict__ res, const typename E::S* __restrict__ weight,
                            int hidden, int64_t x_row_stride, float eps) {
   using S = typename E::S;
   using P = Pack<S, VEC>;
+  constexpr int kStagedPacks = kStageBytes / static_cast<int>(sizeof(P));
+  __shared__ P staged[kStagedPacks];
   __shared__ float scratch[kMaxThreads / 64];
 
   const int64_t row = blockIdx.x;
   const int packs = hidden / VEC;
+  const int window = min(packs, kStagedPacks);
   const P* xr = reinterpret_cast<const P*>(x + row * x_row_stride);
   P* rr = HAS_RES ? reinterpret_cast<P*>(res + row * static_cast<int64_t>(hidden)) : nullptr;
   P* orow = reinterpret_cast<P*>(out + row * static_cast<int64_t>(hidden));
   const P* wr = reinterpret_cast<const P*>(weight);
 
-  float sum_sq = 0.0f;
-  for (int p = threadIdx.x; p < packs; p += blockDim.x) {
-    P a = xr[p];
+  // The value the residual stream carries for pack p: dtype(x + residual), or x.
+  auto rounded_sum = [&](int p) {
+    P v = xr[p];
     if constexpr (HAS_RES) {
       const P r = rr[p];
 #pragma unroll
-      for (int j = 0; j < VEC; ++j) a.v[j] = E::from_f32(E::to_f32(a.v[j]) + E::to_f32(r.v[j]));
-      rr[p] = a;
+      for (int j = 0; j < VEC; ++j) v.v[j] = E::from_f32(E::to_f32(v.v[j]) + E::to_f32(r.v[j]));
     }
+    return v;
+  };
+
+  float sum_sq = 0.0f;
+  for (int p = threadIdx.x; p < packs; p += blockDim.x) {
+    const P v = rounded_sum(p);
 #pragma unroll
     for (int j = 0; j < VEC; ++j) {
-      const float f = E::to_f32(a.v[j]);
+      const float f = E::to_f32(v.v[j]);
       sum_sq += f * f;
+    }
+    if (p < window) {
+      staged[p] = v;
+      if constexpr (HAS_RES) rr[p] = v;
     }
   }
   const float rstd = inv_rms(block_sum(sum_sq, scratch), hidden, eps);
 
-  const P* src = HAS_RES ? rr : xr;
   for (int p = threadIdx.x; p < packs; p += blockDim.x) {
-    const P a = src[p];
+    P v;
+    if (p < window) {
+      v = staged[p];
+    } else {
+      v = rounded_sum(p);
+      if constexpr (HAS_RES) rr[p] = v;
+    }
     const P g = wr[p];
     P o;
 #pragma unroll
-    for (int j = 0; j < VEC; ++j) o.v[j] = E::from_f32((E::to_f32(a.v[j]) * rstd) * E::to_f32(g.v[j]));
+    for (int j = 0; j < VEC; ++j) o.v[j] = E::from_f32((E::to_f32(v.v[j]) * rstd) * E::to_f32(g.v[j]));
     orow[p] = o;
   }
 }
@@ -226,7 +255,7 @@ int launch_vec(void* out, const void* x, void* res, const void* w, int64_t rows,
   } else if (npack <= 8) {
     rms_norm_reg_kernel<E, VEC, 8, HAS_RES><<<grid, threads, 0, stream>>>(o, xi, r, wi, hidden, x_row_stride, eps);
   } else {
-    rms_norm_stream_kernel<E, VEC, HAS_RES><<<grid, kMaxThreads, 0, stream>>>(o, xi, r, wi, hidden, x_row_stride, eps);
+    rms_norm_staged_kernel<E, VEC, HAS_RES><<<grid, kMaxThreads, 0, stream>>>(o, xi, r, wi, hidden, x_row_stride, eps);
   }
   return check_launch("rms_norm kernel launch");
 }

@@ -59,38 +59,69 @@ kl_stream_t current_stream(const at::Device& device) {
       c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(device.index()).stream());
 }
 
-// Same checks as rms_norm_impl in the reference (csrc/torch_bindings.cpp:31-49).
+// The argument contract of the reference's RMSNorm operators
+// (csrc/torch_bindings.cpp:31-49 there): GPU tensors on one device and of one
+// dtype; x's last dimension contiguous; out and weight contiguous, out shaped
+// like x, one weight per hidden element; a residual contiguous and shaped like x.
+void check_norm_args(const at::Tensor& out, const at::Tensor& x, const at::Tensor* residual,
+                     const at::Tensor& weight) {
+  for (const at::Tensor* t : {&x, &weight, &out, residual}) {
+    if (t == nullptr) continue;
+    TORCH_CHECK(t->is_cuda(), "tensors must be on the GPU");
+    TORCH_CHECK(t->device() == x.device(), "tensors must share a device");
+    TORCH_CHECK(t->scalar_type() == x.scalar_type(), "x, weight, out and residual must share a dtype");
+  }
+  TORCH_CHECK(x.dim() >= 1 && x.stride(-1) == 1, "x must have a contiguous last dimension");
+  TORCH_CHECK(weight.is_contiguous() && weight.numel() == x.size(-1), "weight needs one contiguous value per hidden "
+              "element (", weight.numel(), " values, hidden ", x.size(-1), ")");
+  TORCH_CHECK(out.is_contiguous() && out.sizes() == x.sizes(), "out must be contiguous and shaped like x");
+  if (residual != nullptr) {
+    TORCH_CHECK(residual->is_contiguous() && residual->sizes() == x.sizes(),
+                "residual must be contiguous and shaped like x");
+  }
+}
+
+// x as `count` rows of its last dimension, row i at data + i * stride
+// elements. The kernels take one row stride, which the strides of x's
+// leading dimensions give when they nest (each steps over the next one's
+// span; size-1 dimensions are free). Otherwise, or when rows would overlap,
+// the rows are read from a contiguous copy: x is only read, so the result is
+// the same.
+struct NormRows {
+  at::Tensor data;  // x, or its contiguous copy
+  int64_t count;
+  int64_t stride;
+};
+
+NormRows norm_rows(const at::Tensor& x) {
+  const int64_t hidden = x.size(-1);
+  const int64_t count = hidden > 0 ? x.numel() / hidden : 0;
+  int64_t stride = hidden;  // a single row
+  bool nested = true;
+  int64_t inner_size = 0, inner_stride = 0;  // the next non-trivial dimension inward
+  for (int64_t d = x.dim() - 2; d >= 0; --d) {
+    if (x.size(d) == 1) continue;
+    if (inner_size == 0) {
+      stride = x.stride(d);  // the innermost leading dimension steps from row to row
+    } else if (x.stride(d) != inner_stride * inner_size) {
+      nested = false;
+    }
+    inner_size = x.size(d);
+    inner_stride = x.stride(d);
+  }
+  if (!nested || (count > 1 && stride < hidden)) return {x.contiguous(), count, hidden};
+  return {x, count, stride};
+}
+
 void rms_norm_impl(at::Tensor& out, const at::Tensor& x, at::Tensor* residual, const at::Tensor& weight,
                    double eps) {
-  TORCH_CHECK(x.is_cuda() && weight.is_cuda() && out.is_cuda(), "tensors must be on the GPU");
-  TORCH_CHECK(x.device() == weight.device() && x.device() == out.device(), "tensors must share a device");
-  TORCH_CHECK(x.dim() >= 1 && x.stride(-1) == 1, "x must have a contiguous last dimension");
-  TORCH_CHECK(out.is_contiguous() && weight.is_contiguous(), "out and weight must be contiguous");
-  const int64_t hidden = x.size(-1);
-  TORCH_CHECK(weight.numel() == hidden, "weight size ", weight.numel(), " != hidden ", hidden);
-  TORCH_CHECK(out.sizes() == x.sizes(), "out must match x");
-  TORCH_CHECK(x.scalar_type() == weight.scalar_type() && x.scalar_type() == out.scalar_type(),
-              "x, weight and out must share a dtype");
-
-  // Rows of x may be strided (a slice); view everything as [rows, hidden].
-  const at::Tensor x2 = x.dim() == 2 ? x : x.reshape({-1, hidden});
-  TORCH_CHECK(x2.stride(-1) == 1, "x cannot be viewed as rows with a contiguous last dim");
-  void* res_ptr = nullptr;
-  if (residual != nullptr) {
-    TORCH_CHECK(residual->is_cuda() && residual->device() == x.device(), "residual must be on x's device");
-    TORCH_CHECK(residual->is_contiguous() && residual->sizes() == x.sizes() &&
-                    residual->scalar_type() == x.scalar_type(),
-                "residual must be contiguous, same shape and dtype as x");
-    res_ptr = residual->data_ptr();
-  }
-  if (x2.numel() == 0) return;
-
+  check_norm_args(out, x, residual, weight);
+  const NormRows rows = norm_rows(x);
+  if (rows.count == 0) return;
   const c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
-  const int64_t rows = x2.size(0);
-  const int64_t stride = rows > 1 ? x2.stride(0) : hidden;
-  check_status(kl_rms_norm(to_kl_dtype(x.scalar_type()), out.data_ptr(), x2.data_ptr(), res_ptr,
-                           weight.data_ptr(), rows, hidden, stride, static_cast<float>(eps),
-                           current_stream(x.device())),
+  check_status(kl_rms_norm(to_kl_dtype(x.scalar_type()), out.data_ptr(), rows.data.data_ptr(),
+                           residual != nullptr ? residual->data_ptr() : nullptr, weight.data_ptr(), rows.count,
+                           x.size(-1), rows.stride, static_cast<float>(eps), current_stream(x.device())),
                "rms_norm");
 }
 

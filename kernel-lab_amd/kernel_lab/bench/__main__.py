@@ -99,6 +99,17 @@ class Timer:
 SUSPECT_FRACTION = 0.92
 
 
+def _checked(fn: Callable[[], torch.Tensor], expected: torch.Tensor, atol: float) -> tuple[float | None, str]:
+    """Runs fn once and compares it with the baseline's output: (max |error|,
+    "" when within atol, else why it will not be timed)."""
+    try:
+        got = fn()
+    except Exception as exc:  # unsupported shape, out of memory, no such backend
+        return None, f"skipped: {exc}"[:120]
+    err = float((got.float() - expected.float()).abs().max())
+    return err, "" if err <= atol else "WRONG RESULT, not timed"  # NaN is never <= atol
+
+
 def measure(
     kernel: str,
     shape: str,
@@ -109,37 +120,33 @@ def measure(
     atol: float,
     timer: Callable[[Callable[[], object]], float],
 ) -> list[Row]:
-    # A copy: implementations may write into one shared output tensor.
+    """Check every implementation against the baseline's output first, then
+    time only those that agree (a wrong result is never reported as a speed),
+    and report each with bandwidth from the byte model and speedup over the
+    baseline. Implementations may write into one shared output tensor, so
+    the baseline's result is copied before the others run."""
     expected = impls[baseline]().clone()
-    rows: list[Row] = []
-    base_us = None
-    for name, fn in impls.items():
-        try:
-            out = fn()
-            err = (out.float() - expected.float()).abs().max().item()
-            if not err <= atol:  # NaN fails too
-                rows.append(Row(kernel, shape, name, None, None, None, None, err, "WRONG RESULT, not timed"))
-                continue
-            us = timer(fn)
-        except Exception as exc:  # unsupported shape, out of memory
-            rows.append(Row(kernel, shape, name, None, None, None, None, None, f"skipped: {exc}"[:120]))
+    verdict = {name: _checked(fn, expected, atol) for name, fn in impls.items()}
+    elapsed: dict[str, float] = {}
+    for name, (err, why) in verdict.items():
+        if not why:
+            elapsed[name] = timer(impls[name])
+    base_us = elapsed.get(baseline)
+    rows = []
+    for name, (err, why) in verdict.items():
+        us = elapsed.get(name)
+        if us is None:
+            rows.append(Row(kernel, shape, name, None, None, None, None, err, why))
             continue
-        w = work[name] if isinstance(work, dict) else work
-        gbps = w.bytes / (us * 1e-6) / 1e9
-        if name == baseline:
-            base_us = us
-        note = ""
-        if peak and gbps > SUSPECT_FRACTION * peak.dram_gbps:
-            # docs/gpu-runbook.md:75-76 of the reference: a wrong byte count,
-            # or data served from cache instead of HBM.
-            note = "above 92 % of peak: check the byte count and cache residency"
-        rows.append(
-            Row(kernel, shape, name, round(us, 2), round(gbps, 1),
-                round(100 * gbps / peak.dram_gbps, 1) if peak else None, None, err, note)
-        )
-    for row in rows:
-        if row.us and base_us:
-            row.speedup = round(base_us / row.us, 2)
+        nbytes = (work[name] if isinstance(work, dict) else work).bytes
+        gbps = nbytes / us / 1e3  # bytes per microsecond -> GB/s
+        share = gbps / peak.dram_gbps if peak else None
+        # Above ~92 % of the spec sheet the byte count is wrong or the data came
+        # from cache, not HBM (the original runbook's check, docs/gpu-runbook.md:75-76).
+        flag = "above 92 % of peak: check the byte count and cache residency" if share and share > SUSPECT_FRACTION else ""
+        rows.append(Row(kernel, shape, name, round(us, 2), round(gbps, 1),
+                        None if share is None else round(100 * share, 1),
+                        round(base_us / us, 2) if base_us else None, err, flag))
     return rows
 
 
@@ -199,25 +206,64 @@ def rmsnorm_suite(dtype: torch.dtype, peak: GPUPeak | None, timer, compile_basel
 # ------------------------------------------------------- decode attention
 
 
-def torch_paged_decode(q, k_cache, v_cache, block_table, seq_lens, scale):
-    """What plain PyTorch does: gather the pages into padded K/V, mask, softmax(QK^T)V.
+def _padded_kv(cache: torch.Tensor, block_table: torch.Tensor) -> torch.Tensor:
+    """Every sequence's pages gathered into one padded [B, L, Hkv, D] tensor
+    (L = block-table width x page size); tokens past a sequence's length are
+    whatever its last and padding pages hold."""
+    batch, width = block_table.shape
+    return cache[block_table.long()].reshape(batch, width * cache.shape[1], cache.shape[2], cache.shape[3])
 
-    Products run on contiguous operands (K^T is materialised): batched 16-bit
-    products with a transposed right operand are avoided on this platform.
+
+def _valid_tokens(block_table: torch.Tensor, seq_lens: torch.Tensor, page: int) -> torch.Tensor:
+    positions = torch.arange(block_table.shape[1] * page, device=seq_lens.device)
+    return positions[None, :] < seq_lens[:, None].long()  # [B, L]
+
+
+def torch_sdpa_decode(q, k_cache, v_cache, block_table, seq_lens, scale, padded: bool = True):
+    """The original harness's PyTorch baseline (kernel_lab/bench/__main__.py:128-139
+    there): pages gathered into padded K/V, then scaled_dot_product_attention.
+
+    Only SDPA's fused kernels may serve the call: its math fallback runs
+    batched 16-bit products on a transposed view of K, a form that has faulted
+    the GPU on this platform. On this build's SDPA (probed on MI355X, fp16 and
+    bf16), the flash kernel takes grouped-query heads only without a mask,
+    and the memory-efficient kernel takes a mask only with K/V expanded to
+    every query head. So a batch whose sequences all fill the block table
+    (`padded` False) runs flash with grouped heads; otherwise K/V are expanded
+    and the padding masked.
     """
-    batch, hq, d = q.shape
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    batch, hq, _ = q.shape
     page, hkv = k_cache.shape[1], k_cache.shape[2]
-    group = hq // hkv
-    max_len = block_table.shape[1] * page
-    bt = block_table.long()
-    k = k_cache[bt].reshape(batch, max_len, hkv, d).permute(0, 2, 3, 1).contiguous()  # [B, Hkv, D, L]
-    v = v_cache[bt].reshape(batch, max_len, hkv, d).permute(0, 2, 1, 3).contiguous()  # [B, Hkv, L, D]
-    qg = q.reshape(batch, hkv, group, d)
-    scores = torch.matmul(qg, k).float() * scale  # [B, Hkv, G, L]
-    mask = torch.arange(max_len, device=q.device)[None, :] < seq_lens[:, None].long()
-    scores = scores.masked_fill(~mask[:, None, None, :], float("-inf"))
-    probs = torch.softmax(scores, dim=-1).to(q.dtype)
-    return torch.matmul(probs, v).reshape(batch, hq, d)
+    keys = _padded_kv(k_cache, block_table).transpose(1, 2)  # [B, Hkv, L, D]
+    values = _padded_kv(v_cache, block_table).transpose(1, 2)
+    with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+        if not padded:
+            out = torch.nn.functional.scaled_dot_product_attention(
+                q.unsqueeze(2), keys, values, scale=scale, enable_gqa=True
+            )
+        else:
+            keep = _valid_tokens(block_table, seq_lens, page)[:, None, None, :]
+            out = torch.nn.functional.scaled_dot_product_attention(
+                q.unsqueeze(2), keys.repeat_interleave(hq // hkv, dim=1), values.repeat_interleave(hq // hkv, dim=1),
+                attn_mask=keep, scale=scale,
+            )
+    return out.squeeze(2)
+
+
+def torch_paged_decode(q, k_cache, v_cache, block_table, seq_lens, scale):
+    """Plain PyTorch without SDPA: the same gather, then softmax(q K^T) V as two
+    batched products on contiguous operands (K^T materialised), the products
+    that are safe for 16-bit data on this platform."""
+    batch, hq, d = q.shape
+    hkv = k_cache.shape[2]
+    keys_t = _padded_kv(k_cache, block_table).permute(0, 2, 3, 1).contiguous()  # [B, Hkv, D, L]
+    values = _padded_kv(v_cache, block_table).permute(0, 2, 1, 3).contiguous()  # [B, Hkv, L, D]
+    scores = torch.matmul(q.reshape(batch, hkv, hq // hkv, d), keys_t).float() * scale  # [B, Hkv, G, L]
+    keep = _valid_tokens(block_table, seq_lens, k_cache.shape[1])[:, None, None, :]
+    probs = torch.softmax(scores.masked_fill(~keep, float("-inf")), dim=-1).to(q.dtype)
+    return torch.matmul(probs, values).reshape(batch, hq, d)
 
 
 def decode_cases(dtype: torch.dtype) -> list[tuple[str, list[int], int, int, torch.dtype]]:
@@ -282,6 +328,14 @@ def decode_suite(
         # The gather baseline materialises padded K/V; skip it where that would be huge.
         gather_bytes = 2 * kv.block_table.numel() * page * hkv * d * elem
         if gather_bytes <= baseline_max_bytes:
+            padded = any(n != kv.block_table.shape[1] * page for n in lens)
+            sdpa = lambda a=args, s=scale, p=padded: torch_sdpa_decode(*a, s, p)  # noqa: E731
+            try:
+                sdpa()
+                impls["torch (gather + SDPA)"] = sdpa  # the original harness's baseline
+            except RuntimeError as exc:  # no fused SDPA kernel for this case
+                rows.append(Row("paged_decode", label, "torch (gather + SDPA)", None, None, None, None, None,
+                                f"skipped: {exc}"[:120]))
             impls["torch (gather + matmul)"] = lambda a=args, s=scale: torch_paged_decode(*a, s)
         impls["hip split-KV (planner)"] = lambda a=args, s=scale, o=out: ops.paged_decode_attention(*a, s, out=o)
         if dt != torch.float32:
@@ -545,22 +599,28 @@ def attribute_trace(trace_csv: Path, order: list[dict]) -> str:
 # --------------------------------------------------------------------- report
 
 
+def _cell(value: float | None, unit: str = "") -> str:
+    return "-" if value is None else f"{value}{unit}"
+
+
+# (heading, alignment, cell) for each column of the results table.
+_COLUMNS: tuple[tuple[str, str, Callable[[Row], str]], ...] = (
+    ("Kernel", "---", lambda r: r.kernel),
+    ("Shape", "---", lambda r: r.shape),
+    ("Implementation", "---", lambda r: f"{r.impl} ({r.note})" if r.note else r.impl),
+    ("Time (µs)", "---:", lambda r: _cell(r.us)),
+    ("GB/s", "---:", lambda r: _cell(r.gbps)),
+    ("% peak BW", "---:", lambda r: _cell(r.pct_peak_bw, "%")),
+    ("Speedup", "---:", lambda r: _cell(r.speedup, "x")),
+    ("Max err", "---:", lambda r: "-" if r.max_abs_err is None else f"{r.max_abs_err:.1e}"),
+)
+
+
 def to_markdown(rows: list[Row], header: str) -> str:
-    lines = [
-        header,
-        "",
-        "| Kernel | Shape | Implementation | Time (µs) | GB/s | % peak BW | Speedup | Max err |",
-        "|---|---|---|---:|---:|---:|---:|---:|",
-    ]
-    for r in rows:
-        fmt = lambda v, suffix="": "-" if v is None else f"{v}{suffix}"  # noqa: E731
-        err = "-" if r.max_abs_err is None else f"{r.max_abs_err:.1e}"
-        impl = r.impl if not r.note else f"{r.impl} ({r.note})"
-        lines.append(
-            f"| {r.kernel} | {r.shape} | {impl} | {fmt(r.us)} | {fmt(r.gbps)} | {fmt(r.pct_peak_bw, '%')} "
-            f"| {fmt(r.speedup, 'x')} | {err} |"
-        )
-    return "\n".join(lines) + "\n"
+    """A markdown table of the rows under `header`; untimed rows show why."""
+    table = ["| " + " | ".join(c[0] for c in _COLUMNS) + " |", "|" + "|".join(c[1] for c in _COLUMNS) + "|"]
+    table += ["| " + " | ".join(c[2](r) for c in _COLUMNS) + " |" for r in rows]
+    return "\n".join([header, "", *table]) + "\n"
 
 
 def main(argv: list[str] | None = None) -> int:

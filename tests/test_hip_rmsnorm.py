@@ -121,14 +121,51 @@ def test_zero_rows_stay_finite(gpu_ops):
     assert torch.isfinite(gpu_ops.rms_norm(x, torch.ones(32, device="cuda"), eps=1e-6)).all()
 
 
-@pytest.mark.parametrize("hidden", [16384, 65536, 100000])
-def test_wide_rows(gpu_ops, hidden):
-    """Rows past the register-resident limit take the two-pass kernel."""
-    x, r, w = make((3, hidden), torch.bfloat16, seed=hidden)
-    out, res = gpu_ops.fused_add_rms_norm(x, r, w)
-    ref_out, ref_res = ref.fused_add_rms_norm(x.cpu(), r.cpu(), w.cpu())
-    assert torch.equal(res.cpu(), ref_res)
-    torch.testing.assert_close(out.cpu(), ref_out, **tolerance(torch.bfloat16))
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize(
+    ("hidden", "fused"),
+    [(16384, True), (65536, True), (100000, True), (300000, True), (300000, False), (40001, True), (12289, False)],
+)
+def test_wide_rows(gpu_ops, hidden, fused, dtype):
+    """Rows past the register-resident limit (16-bit > 65,536, fp32 > 32,768
+    aligned; > 8,192 unaligned) take the LDS-staged kernel: the row's first
+    48 KiB come back from LDS and the rest is formed again from x and the
+    residual, whose new value must still be written exactly once."""
+    x, r, w = make((3, hidden), dtype, seed=hidden)
+    if fused:
+        out, res = gpu_ops.fused_add_rms_norm(x, r, w)
+        ref_out, ref_res = ref.fused_add_rms_norm(x.cpu(), r.cpu(), w.cpu())
+        assert torch.equal(res.cpu(), ref_res)
+    else:
+        out = gpu_ops.rms_norm(x, w)
+        ref_out = ref.rms_norm(x.cpu(), w.cpu())
+    torch.testing.assert_close(out.cpu(), ref_out, **tolerance(dtype))
+    if dtype != torch.float32:
+        assert ulp_distance(out.cpu(), ref_out) <= 1
+
+
+@pytest.mark.parametrize(
+    "layout",
+    ["sliced rows", "every other middle row", "transposed leading dims", "size-one middle", "expanded rows"],
+)
+def test_rows_of_any_leading_layout(gpu_ops, layout):
+    """The operator addresses x's rows with one stride when its leading
+    dimensions nest (each spans the next), and reads a contiguous copy when
+    they do not (or rows would overlap); either way the result is the oracle's."""
+    base = torch.randn(4, 6, 288, device="cuda", dtype=torch.float16)
+    w = (1 + 0.1 * torch.randn(256, device="cuda")).half()
+    x = {
+        "sliced rows": base[:, :, :256],  # row stride 288
+        "every other middle row": base[:, ::2, :256],  # nested: 1728 = 576 x 3
+        "transposed leading dims": base.transpose(0, 1)[:, :, :256],  # 288 != 1728 x 4: copied
+        "size-one middle": base[:, 2:3, :256],  # a size-1 dimension has any stride
+        "expanded rows": base[0, 0, :256].expand(5, 256),  # row stride 0: copied
+    }[layout]
+    out = torch.empty(x.shape, device="cuda", dtype=torch.float16)
+    torch.ops.kernel_lab.rms_norm(out, x, w, 1e-6)
+    want = ref.rms_norm(x.cpu(), w.cpu())
+    torch.testing.assert_close(out.cpu(), want, **tolerance(torch.float16))
+    assert ulp_distance(out.cpu(), want) <= 1
 
 
 def test_validation_errors(gpu_ops):
