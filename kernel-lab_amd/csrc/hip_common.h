@@ -111,6 +111,11 @@ constexpr int kDppQuadSwap1 = 0xB1;  // quad_perm [1,0,3,2]: lane ^ 1
 constexpr int kDppQuadSwap2 = 0x4E;  // quad_perm [2,3,0,1]: lane ^ 2
 constexpr int kDppRowRor4 = 0x124;
 constexpr int kDppRowRor8 = 0x128;
+// row_shr:n moves lane i's value to lane i + n of the same 16-lane row.
+constexpr int kDppRowShr1 = 0x111;
+constexpr int kDppRowShr2 = 0x112;
+constexpr int kDppRowShr4 = 0x114;
+constexpr int kDppRowShr8 = 0x118;
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
@@ -137,6 +142,25 @@ __device__ __forceinline__ float row16_max(float v) {
   v = fmaxf(v, dpp<kDppRowRor4>(v));
   v = fmaxf(v, dpp<kDppRowRor8>(v));
   return v;
+}
+
+// Inclusive prefix sum over the wave's 64 lanes (lane i gets v[0] + ... +
+// v[i]) without LDS: a Hillis-Steele scan inside each 16-lane row by DPP row
+// shifts (a lane shifted in from before the row's start reads 0), then every
+// row adds the totals of the rows before it, read from lanes 15, 31 and 47.
+// Having no LDS instruction, it leaves the LDS/scalar-memory counter alone, so
+// a scalar load issued before it stays in flight. Checked on MI355X against
+// sequential sums (unit steps, lone values in lanes 0 and 63, random signed).
+__device__ __forceinline__ int wave_prefix_sum(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, kDppRowShr1, 0xF, 0xF, true);
+  v += __builtin_amdgcn_update_dpp(0, v, kDppRowShr2, 0xF, 0xF, true);
+  v += __builtin_amdgcn_update_dpp(0, v, kDppRowShr4, 0xF, 0xF, true);
+  v += __builtin_amdgcn_update_dpp(0, v, kDppRowShr8, 0xF, 0xF, true);
+  const int r0 = __builtin_amdgcn_readlane(v, 15);
+  const int r1 = __builtin_amdgcn_readlane(v, 31);
+  const int r2 = __builtin_amdgcn_readlane(v, 47);
+  const int row = __lane_id() >> 4;
+  return v + (row >= 1 ? r0 : 0) + (row >= 2 ? r1 : 0) + (row >= 3 ? r2 : 0);
 }
 
 // Sum over the whole wave64, returned wave-uniform. The four row sums are
@@ -184,6 +208,14 @@ constexpr int kBufferDword3 = 0x00020000;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), 0x7fffffff,
+                                           kBufferDword3);
+}
+
+// A resource covering exactly `bytes` bytes from `base`: a load at an offset
+// past them returns 0 without touching memory (the hardware's range check), so
+// lanes beyond the end of an array need no branch around their load.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_bytes(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(bytes),
                                            kBufferDword3);
 }
 

@@ -914,15 +914,7 @@ __device__ __forceinline__ int seq_pages_uniform(const DecodeArgs& a, int b) {
   return len > 0 ? (len + a.page_size - 1) / a.page_size : 0;
 }
 
-__device__ __forceinline__ int wave_incl_scan(int v) {
-  const int lane = __lane_id();
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int t = __shfl_up(v, d, 64);
-    if (lane >= d) v += t;
-  }
-  return v;
-}
+__device__ __forceinline__ int wave_incl_scan(int v) { return wave_prefix_sum(v); }
 
 __device__ __forceinline__ int64_t balanced_per(const DecodeArgs& a, int64_t total) {
   return max(static_cast<int64_t>(kMinPagesPerBalancedWg), (total + a.grid - 1) / a.grid);
@@ -1002,14 +994,23 @@ __device__ __forceinline__ Start schedule_start(const DecodeArgs& a, int units_p
   if (a.batch <= 64 * kScanChunks) {
     int len[kScanChunks], pl[kScanChunks], incl[kScanChunks];
     int64_t before[kScanChunks];
-    // Chunks past the batch are skipped (uniform branches): a scan is a
-    // chain of cross-lane shuffles, not free.
+    // All chunks' seq_lens loads are issued before any is used, through a
+    // resource that ends with the array: lanes past the batch read 0 with no
+    // branch. (A per-lane branch around each load, with its clamp inside,
+    // made the compiler wait for each load in turn: one memory round trip
+    // per 64 sequences.) Chunks past the batch are skipped by uniform
+    // branches: a scan is a chain of cross-lane steps, not free.
+    const auto lens_rsrc = make_rsrc_bytes(uniform_ptr(a.seq_lens), static_cast<uint32_t>(a.batch) * 4u);
+    int raw[kScanChunks];
 #pragma unroll
     for (int k = 0; k < kScanChunks; ++k) {
-      const int b = 64 * k + lane;
-      len[k] = 0;
-      if (64 * k < a.batch) len[k] = b < a.batch ? clamped_len(a, a.seq_lens[b]) : 0;
+      raw[k] = 0;
+      if (64 * k < a.batch) {
+        raw[k] = __builtin_bit_cast(int, buffer_load_f32(lens_rsrc, static_cast<uint32_t>((64 * k + lane) * 4)));
+      }
     }
+#pragma unroll
+    for (int k = 0; k < kScanChunks; ++k) len[k] = clamped_len(a, raw[k]);
     int64_t total = 0;
 #pragma unroll
     for (int k = 0; k < kScanChunks; ++k) {
@@ -1119,7 +1120,25 @@ __global__ void __launch_bounds__(PAIR * balanced_waves<D>() * 64, (mfma_waves_p
   const int half = PAIR == 2 ? wave_id() / W : 0;
   const int hp = a.num_kv_heads * a.head_groups / PAIR;  // list units per sequence
   const int w = PAIR == 2 ? paired_list_wg(a, hp) : static_cast<int>(blockIdx.x);
+  // Where this workgroup would start if every sequence had max_pages pages:
+  // its block-table entry is fetched now, alongside the seq_lens loads the
+  // schedule waits for. On such a batch the guess is exact and the segment's
+  // own load of the entry finds it cached, instead of making a second
+  // dependent trip to memory after the schedule (the uniform-split kernel
+  // needs no guess: its first page is known before it reads seq_lens). A wrong
+  // guess costs one load inside the block table.
+  int32_t guessed_page = 0;
+  {
+    const int64_t seq_span = static_cast<int64_t>(hp) * a.max_pages;
+    const int64_t full = static_cast<int64_t>(a.batch) * seq_span;
+    const int64_t pos = static_cast<int64_t>(w) * balanced_per(a, full);
+    if (pos < full) {
+      const int gb = static_cast<int>(pos / seq_span);
+      guessed_page = as_constant(a.block_table + static_cast<int64_t>(gb) * a.bt_stride)[pos % a.max_pages];
+    }
+  }
   const Start st = schedule_start(a, hp, w);
+  asm volatile("; block-table entry prefetched: %0" ::"s"(guessed_page));
   if (a.arrivals != nullptr) {
     // No merge kernel follows: empty sequences get their zeros here, sequence
     // b from workgroup b % grid (up to 64 * kScanChunks from the schedule's scan).
@@ -1147,8 +1166,13 @@ __global__ void __launch_bounds__(PAIR * balanced_waves<D>() * 64, (mfma_waves_p
 
   while (pos < end && b < a.batch) {
     // b is pages-bearing: the start and the advance below skip empty sequences.
-    const int r = static_cast<int>((pos - base) / n);
-    const int page0 = static_cast<int>(pos - base - static_cast<int64_t>(r) * n);
+    // The offset inside sequence b's units is below hp * max_pages, so 32-bit
+    // arithmetic splits it into a unit and a page (a 64-bit division here,
+    // scalar and in software, cost ~0.5 us before every segment's first load).
+    const uint32_t off = static_cast<uint32_t>(pos - base);
+    const uint32_t ru = off / static_cast<uint32_t>(n);
+    const int r = static_cast<int>(ru);
+    const int page0 = static_cast<int>(off - ru * static_cast<uint32_t>(n));
     const int64_t unit_base = base + static_cast<int64_t>(r) * n;
     const int page1 = static_cast<int>(min(static_cast<int64_t>(n), end - unit_base));
 
@@ -1157,8 +1181,9 @@ __global__ void __launch_bounds__(PAIR * balanced_waves<D>() * 64, (mfma_waves_p
     // land in VGPRs and every K/V load becomes a per-lane waterfall loop.
     Unit u;
     u.b = __builtin_amdgcn_readfirstlane(b);
-    u.kvh = __builtin_amdgcn_readfirstlane((r / a.head_groups) * PAIR + half);
-    u.hg = __builtin_amdgcn_readfirstlane(r % a.head_groups);
+    const int rkv = a.head_groups == 1 ? r : r / a.head_groups;  // one head group is the common case
+    u.kvh = __builtin_amdgcn_readfirstlane(rkv * PAIR + half);
+    u.hg = __builtin_amdgcn_readfirstlane(r - rkv * a.head_groups);
     u.split = 0;
     u.seq_len = __builtin_amdgcn_readfirstlane(len);
     u.page_begin = __builtin_amdgcn_readfirstlane(page0);
@@ -1172,7 +1197,9 @@ __global__ void __launch_bounds__(PAIR * balanced_waves<D>() * 64, (mfma_waves_p
     dst.o_head_stride = D;
     dst.lse_head_stride = 1;
 
-    __syncthreads();  // the previous segment's wave 0 may still read LDS
+    // The previous segment's waves may still read LDS; before the first
+    // segment nothing has used it (the schedule needs no LDS), so no barrier.
+    if (pos != st.pos) __syncthreads();
     mfma_segment<E, KVF, D, NT, W>(a, lds + half * MfmaLds<D, NT, W>::kBytes, u, dst, wave_id() - half * W);
     if (NT == 1 && !dst.final && a.arrivals != nullptr) {  // see kFusedMergeMaxHeads
       // The unit's segments are workgroups w0 .. w1 (slots (w + list unit) * PAIR + half).
