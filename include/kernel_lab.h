@@ -99,7 +99,9 @@ int kl_rms_norm(kl_dtype dtype, void* out, const void* x, void* residual, const 
  *   out_num_splits   (host pointer) uniform splits the launch will use, or 0
  *                    when it balances pages across sequences on the device
  *                    (chosen for fp16/bf16 when there are fewer
- *                    (sequence, KV head) units than compute units)
+ *                    (sequence, KV head) units than compute units, or when a
+ *                    full batch's table spans >= 256 pages and the balanced
+ *                    workspace stays within 16 MiB)
  *   out_workspace    (host pointer) bytes of device workspace the launch needs
  *                    (0 when the launch needs none)
  */

@@ -117,6 +117,11 @@ constexpr int kMinPagesPerBalancedWg = KL_DECODE_BALANCED_MIN_PAGES;
 // splits to the merge (64/8/128 B=1 ctx 32768, 64 segments: +6 us).
 constexpr int kPairMinPages = 128;
 constexpr int kPairMaxSegments = 16;
+// Full batches take the balanced schedule from this many block-table columns
+// on (see balance_override), as long as its workspace stays within
+// kAutoBalanceMaxWorkspace (the no-allocation entry point's array).
+constexpr int kBalanceMinPages = 256;
+constexpr size_t kAutoBalanceMaxWorkspace = size_t{16} << 20;
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct DecodeArgs {
@@ -1739,21 +1744,23 @@ bool pairing_enabled() {
   return v == nullptr || v[0] != '0';
 }
 
-// The planner's choice for fp16/bf16 batches whose units fill the device:
-// uniform splits sized from the block table's width (default), or the
-// balanced schedule with KL_DECODE_BALANCE_ALWAYS=1 in the environment (read
-// on every call; =0 forces uniform). Measured on MI355X (events, us, uniform
-// -> balanced): even batches 164.5 -> 165.0 (32/8/128 fp16 B=64 ctx 4096) up
-// to 19.5 -> 20.6 (B=32 ctx 512): the balanced start scans seq_lens before a
-// workgroup knows its first page (2.4 us against 0.85 us for the uniform
-// kernel's one scalar load); ragged lengths U[1, 8192] B=64 238 -> 217, B=32
-// 126 -> 109; one 65,536-token sequence among 63 of 2,048 tokens 1,228 -> 139.
-// Even batches keep the default; callers with uneven lengths pass
-// KL_SPLITS_BALANCED.
-bool balance_always() {
+// The planner's choice for fp16/bf16 batches whose units fill the device
+// (units >= CUs) is the balanced schedule when the block table is long
+// (kBalanceMinPages or more columns) and uniform splits otherwise. The
+// planner cannot see seq_lens, and with uniform splits one long sequence
+// among short ones sets the time: measured on MI355X (events, us, same
+// tensors alternating), one 65,536-token sequence among 63 of 2,048 tokens
+// 1,231 (uniform) vs 142 (balanced), ragged U[1, 8192] B=64 228 vs 207. On an
+// even batch the balanced schedule gives every workgroup the same single unit
+// and costs only its start: 163.4 vs 164.6 (32/8/128 fp16 B=64 ctx 4096),
+// but on short tables that start weighs more (B=32 ctx 512 19.0 vs 19.9,
+// B=128 ctx 2048 169.0 vs 174.2) while the worst skew costs less.
+// KL_DECODE_BALANCE_ALWAYS in the environment (read on every call) overrides
+// the choice for full batches: 1 always balanced, 0 always uniform.
+int balance_override() {
   const char* v = std::getenv("KL_DECODE_BALANCE_ALWAYS");
-  if (v != nullptr && (v[0] == '0' || v[0] == '1')) return v[0] == '1';
-  return KL_DECODE_BALANCE_ALWAYS != 0;
+  if (v != nullptr && (v[0] == '0' || v[0] == '1')) return v[0] == '1' ? 1 : 0;
+  return KL_DECODE_BALANCE_ALWAYS != 0 ? 1 : -1;
 }
 
 // KL_DECODE_FUSED_MERGE=0 sends every split decode to the merge kernels.
@@ -1948,7 +1955,11 @@ int make_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads, int 
                           pair_units * kPairMaxSegments >= cus;
   const bool pairable = mfma && !partials && pairing_enabled() && num_kv_heads % 2 == 0 && head_dim <= 128 &&
                         p->heads_per_wg <= 16 && (units >= 2 * static_cast<int64_t>(cus) || long_pairs);
-  const bool balance = num_splits == KL_SPLITS_BALANCED || (num_splits == 0 && (units < cus || balance_always()));
+  const int full_batch_choice = balance_override();  // 1 balanced, 0 uniform, -1 by table length
+  const bool requested = num_splits == KL_SPLITS_BALANCED;
+  const bool automatic =
+      num_splits == 0 && (units < cus || (full_batch_choice < 0 ? pages >= kBalanceMinPages : full_batch_choice == 1));
+  const bool balance = requested || automatic;
   const bool pair_balanced = pairable && balance;
   if (mfma && !partials && balance) {
     // Requested, or fewer units than CUs: pages balanced across sequences on the device.
@@ -1967,7 +1978,12 @@ int make_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads, int 
     const size_t slots = (static_cast<size_t>(grid) + static_cast<size_t>(lunits)) * (pair_balanced ? 2 : 1);
     p->o_bytes = align_up(slots * p->heads_per_wg * head_dim * sizeof(float));
     p->ws_bytes = p->o_bytes + align_up(slots * p->heads_per_wg * sizeof(float));
-    return ok();
+    // A full batch chosen by table length keeps uniform splits when the
+    // balanced workspace (a slot per workgroup and unit) would be large.
+    const bool by_length = !requested && units >= cus && full_batch_choice < 0;
+    if (!by_length || p->ws_bytes <= kAutoBalanceMaxWorkspace) return ok();
+    p->grid = 0;
+    p->paired = false;
   }
   int s = num_splits;
   if (s == 0) {

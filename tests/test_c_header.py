@@ -24,8 +24,10 @@ int main(void) {
   printf("version %d\n", kl_version());
   printf("ok %s\n", kl_status_string(KL_OK));
   /* Planner: pure host arithmetic with an explicit CU count. */
-  int st = kl_paged_decode_plan(KL_DTYPE_F16, 64, 32, 8, 128, 16, 256, 0, 256, &splits, &ws);
+  int st = kl_paged_decode_plan(KL_DTYPE_F16, 64, 32, 8, 128, 16, 128, 0, 256, &splits, &ws);
   printf("plan64 %d %d %zu\n", st, splits, ws);
+  st = kl_paged_decode_plan(KL_DTYPE_F16, 64, 32, 8, 128, 16, 256, 0, 256, &splits, &ws);
+  printf("plan64long %d %d %d\n", st, splits, ws > 0);
   st = kl_paged_decode_plan(KL_DTYPE_F16, 1, 32, 8, 128, 16, 256, 0, 256, &splits, &ws);
   printf("plan1 %d %d %d\n", st, splits, ws > 0);
   st = kl_paged_decode_plan(KL_DTYPE_F16, 64, 32, 8, 128, 16, 256, KL_SPLITS_BALANCED, 256, &splits, &ws);
@@ -64,6 +66,7 @@ def test_header_compiles_as_c99_and_links(tmp_path):
     assert got["ok"] == "success"
     st, splits, ws = got["plan64"].split()
     assert st == "0" and splits == "1" and int(ws) == 0  # one uniform split fills the device
+    assert got["plan64long"] == "0 0 1"  # a long table on a full batch: balanced
     assert got["plan1"] == "0 0 1"  # balanced schedule for a batch of one
     assert got["planbal"] == "0 0 1"
     assert got["cascade"] == "0 1"
