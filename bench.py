@@ -19,27 +19,42 @@ Two live passes of K steps each, after W warm-up steps:
 * kernel pass: the same K steps with a HIP event pair on the launch stream
   around each operator. Measured on MI355X, an event's timestamp packet
   between two kernels leaves the GPU idle ~5 us (16 us per step, 7 %), so
-  events stay out of the throughput pass; kernel durations are unaffected
-  (the rocprofv3 trace of the same kernels agrees).
+  events stay out of the throughput pass; the pair around one launch also
+  spans its dispatch, 2-4 % above the kernel's traced duration;
+* dominant-kernel pass: K launches of the dominant kernel (decode) back to
+  back inside one event pair on the launch stream; per launch this is the
+  kernel's duration plus the gap between two launches, and it gives the
+  roofline figure.
 
 One JSON line goes to stdout:
 * value: algorithmic bytes of the K steps / wall time of the throughput pass
   (GB/s);
 * kernels: per-operator HIP-event time (kernel pass), GB/s and fraction of the
   8 TB/s peak;
-* roofline: the dominant kernel (decode) against HBM peak, with HBM traffic
-  per launch from the committed rocprofv3 counter summary when present;
+* roofline: the dominant kernel (decode) against HBM peak, with its HBM
+  traffic per launch measured in this run: two child passes of this script
+  under `rocprofv3 --pmc` (FETCH_SIZE, then WRITE_SIZE, one counter per pass,
+  each under its own kill timer) run two decode steps and a 1 GiB elementwise
+  copy, and each counter is scaled by what it reads for the copy, whose bytes
+  are known (on gfx950 FETCH_SIZE reads half of them); null, with the reason,
+  when a pass fails or --no-counters is given;
 * cpu_baseline: the CPU oracle (float32 PyTorch restatement of the original's
-  reference.py) on a bounded sample of the same workload, on this host.
+  reference.py) on a bounded sample of the same workload, on this host's
+  cores (threads = the process's CPU affinity), with the CPU model and the
+  torch version.
 """
 
 from __future__ import annotations
 
 import argparse
+import csv
 import json
 import os
-import re
+import platform
+import shutil
+import subprocess
 import sys
+import tempfile
 import time
 from pathlib import Path
 
@@ -57,19 +72,76 @@ from kernel_lab.kv_cache import device_decode_problem  # noqa: E402
 METRIC = "achieved HBM GB/s + % of peak: paged decode (B=64, ctx 4k) and add-RMSNorm"
 DECODE = {"batch": 64, "ctx": 4096, "num_q_heads": 32, "num_kv_heads": 8, "head_dim": 128, "page_size": 16}
 RMS = {"tokens": 4096, "hidden": 8192}
-TRAFFIC_FILE = ROOT / "profiles" / "decode_b64_ctx4096_fp16.md"
+COPY_BYTES = 1 << 30  # calibration copy: reads and writes this many bytes per dispatch
 
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def read_traffic() -> float | None:
-    """HBM bytes per decode launch from the committed rocprofv3 counter summary."""
-    if not TRAFFIC_FILE.exists():
-        return None
-    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", TRAFFIC_FILE.read_text(), re.M)
-    return float(m.group(1)) if m else None
+def counter_probe(device: torch.device) -> None:
+    """Child mode (under rocprofv3 --pmc): two decode steps of the workload and
+    two 1 GiB elementwise copies, the counters' calibration kernel."""
+    lens, q, kv, _, _, _ = build_inputs(device)
+    out = torch.empty_like(q)
+    for _ in range(2):
+        torch.ops.kernel_lab.paged_decode_attention(out, q, kv.k_cache, kv.v_cache, kv.block_table, kv.seq_lens,
+                                                    DECODE["head_dim"] ** -0.5)
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        torch.add(src, 0.0, out=dst)  # one read and one write of every byte
+    torch.cuda.synchronize()
+
+
+def _counter_means(csv_path: Path, counter: str) -> dict[str, float]:
+    """Mean value per dispatch of `counter` for the decode kernel and for the
+    calibration copy (the two largest elementwise dispatches: the input
+    set-up runs smaller elementwise kernels too)."""
+    decode: list[float] = []
+    elementwise: list[float] = []
+    with open(csv_path, newline="") as f:
+        for row in csv.DictReader(f):
+            if row.get("Counter_Name") != counter:
+                continue
+            name = row.get("Kernel_Name", "")
+            if "decode_mfma" in name:
+                decode.append(float(row["Counter_Value"]))
+            elif "elementwise" in name:
+                elementwise.append(float(row["Counter_Value"]))
+    out = {}
+    if decode:
+        out["decode"] = sum(decode) / len(decode)
+    if len(elementwise) >= 2:
+        out["copy"] = sum(sorted(elementwise)[-2:]) / 2
+    return out
+
+
+def measure_traffic(timeout_s: int = 150) -> tuple[float | None, str]:
+    """HBM bytes per decode launch from this run's counters: one rocprofv3 --pmc
+    pass per counter over a child run of this script, each counter scaled by
+    its reading for the 1 GiB copy. Returns (bytes, how it was obtained)."""
+    prof = shutil.which("rocprofv3")
+    if prof is None:
+        return None, "rocprofv3 not found"
+    per_launch = 0.0
+    notes = []
+    with tempfile.TemporaryDirectory(prefix="kl_pmc_") as tmp:
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            cmd = ["timeout", "-s", "KILL", str(timeout_s), prof, "--pmc", counter, "--kernel-trace", "-f", "csv",
+                   "-d", tmp, "-o", counter, "--", sys.executable, str(Path(__file__).resolve()), "--counter-probe"]
+            log(f"counter pass: {counter}")
+            proc = subprocess.run(cmd, capture_output=True, text=True, cwd=tmp)
+            files = list(Path(tmp).rglob(f"{counter}_counter_collection.csv"))
+            if not files:
+                return None, f"{counter} pass produced no counters (exit {proc.returncode}): {proc.stderr[-200:]}"
+            means = _counter_means(files[0], counter)
+            if "decode" not in means or "copy" not in means:
+                return None, f"{counter} pass: kernels missing from the counter file"
+            scale = COPY_BYTES / (means["copy"] * 1024)  # counters count KiB
+            per_launch += means["decode"] * 1024 * scale
+            notes.append(f"{counter} {means['decode']:.1f} KiB/launch x {scale:.3f} (copy-calibrated)")
+    return per_launch, "; ".join(notes)
 
 
 def build_inputs(device: torch.device):
@@ -114,11 +186,23 @@ def check_outputs(q, kv, out, x, res_before, res_after, w, y) -> dict:
             "rmsnorm_max_abs_err": rms_err}
 
 
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
 def cpu_baseline(q, kv, x, res, w, dec_bytes: float, rms_bytes: float, budget_s: float) -> dict:
-    """The CPU oracle on a bounded sample of the step, on this host's cores."""
+    """The CPU oracle on a bounded sample of the step, on this host's cores:
+    threads = the CPUs this process may run on."""
     from oracle import reference as ref
 
-    threads = torch.get_num_threads()
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
     qc = q[:4].cpu()
     kc, vc = kv.k_cache.cpu(), kv.v_cache.cpu()
     btc, lc = kv.block_table[:4].cpu(), kv.seq_lens[:4].cpu()
@@ -150,6 +234,8 @@ def cpu_baseline(q, kv, x, res, w, dec_bytes: float, rms_bytes: float, budget_s:
         ),
         "decode_gbps": round(dec_bytes / (t_dec * DECODE["batch"] / 4) / 1e9, 3),
         "rmsnorm_gbps": round(rms_bytes / (t_rms * RMS["tokens"] / 256) / 1e9, 3),
+        "cpu_model": _cpu_model(),
+        "torch": torch.__version__,
     }
 
 
@@ -161,6 +247,8 @@ def main(argv: list[str] | None = None) -> int:
     parser.add_argument("--only", choices=["decode", "rmsnorm"], help="time one operator (for profiling runs)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU-oracle timing")
+    parser.add_argument("--no-counters", action="store_true", help="skip the rocprofv3 traffic passes")
+    parser.add_argument("--counter-probe", action="store_true", help=argparse.SUPPRESS)
     args = parser.parse_args(argv)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -180,6 +268,9 @@ def main(argv: list[str] | None = None) -> int:
         return 2
 
     device = torch.device("cuda:0")
+    if args.counter_probe:
+        counter_probe(device)
+        return 0
     name = torch.cuda.get_device_name(device)
     peak = lookup(name) or lookup(torch.cuda.get_device_properties(device).gcnArchName.split(":")[0]) or MI355X
     log(f"device: {name}; peak {peak.dram_gbps} GB/s ({peak.name})")
@@ -257,9 +348,22 @@ def main(argv: list[str] | None = None) -> int:
             # The reference runbook's sanity check (docs/gpu-runbook.md:75-76).
             log(f"warning: {op} above 92 % of peak: check the byte count and cache residency")
 
-    dom_work, dom_ms = (dec_work, dec_ms) if do_dec else (rms_work, rms_ms)
+    dom_work = dec_work if do_dec else rms_work
+    dom_op = (lambda: op_dec(out, q, kv.k_cache, kv.v_cache, kv.block_table, kv.seq_lens, scale)) if do_dec else (
+        lambda: op_rms(y, x, res, w, 1e-6))
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        dom_op()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    dom_ms = e0.elapsed_time(e1) / args.steps
+    log(f"dominant-kernel pass: {args.steps} launches, {dom_ms * 1e3:.2f} us each")
     achieved = dom_work.bytes / (dom_ms * 1e-3) / 1e9
-    traffic = read_traffic() if do_dec else None
+    traffic, traffic_note = None, "not measured (--no-counters or a single-operator run)"
+    if do_dec and not args.no_counters:
+        traffic, traffic_note = measure_traffic()
     roofline = {
         "kernel": "paged_decode_attention" if do_dec else "fused_add_rms_norm",
         "bound": "hbm",
@@ -267,7 +371,10 @@ def main(argv: list[str] | None = None) -> int:
         "peak": peak.dram_gbps,
         "unit": "GB/s",
         "frac": round(achieved / peak.dram_gbps, 4),
-        "traffic": traffic,
+        "us_per_launch": round(dom_ms * 1e3, 2),
+        "traffic": None if traffic is None else round(traffic),
+        "traffic_over_algorithmic": None if traffic is None else round(traffic / dom_work.bytes, 4),
+        "traffic_source": traffic_note,
     }
 
     baseline = None
