@@ -140,7 +140,7 @@ int kl_paged_decode_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_
  * concurrently on any streams. hipStreamPerThread, and streams or captures
  * beyond those counts (reported once on stderr), use the merge launch;
  * results are bit-identical either way. KL_DECODE_FUSED_MERGE=0 in the
- * environment forces the merge launch.
+ * environment forces the merge launch (see kl_paged_decode_reload_options).
  */
 int kl_paged_decode_attention(kl_dtype dtype, void* out, const void* q, const void* k_cache,
                               const void* v_cache, const int32_t* block_table,
@@ -158,6 +158,19 @@ int kl_paged_decode_attention(kl_dtype dtype, void* out, const void* q, const vo
  * launchers do not split sequences.
  */
 int kl_paged_decode_last_merge(void);
+
+/*
+ * Re-reads the decode switches from the environment. The library reads them
+ * once per process, at its first decode call; tests and A/B measurements
+ * that change them afterwards call this. No counterpart in the reference.
+ *   KL_DECODE_FORCE_VALU=1        fp16/bf16 decode on the VALU kernel
+ *   KL_DECODE_PAIRED=0            no two-KV-head workgroups
+ *   KL_DECODE_BALANCE_ALWAYS=1|0  full batches always / never balanced
+ *   KL_DECODE_FUSED_MERGE=0       split sequences merged by a second launch
+ * Results are identical under every setting; only the schedule changes.
+ * Returns KL_OK.
+ */
+int kl_paged_decode_reload_options(void);
 
 /*
  * kl_paged_decode_attention without a workspace argument, for callers that

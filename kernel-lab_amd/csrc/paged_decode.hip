@@ -51,6 +51,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cmath>
+#include <atomic>
 #include <mutex>
 #include <vector>
 #include <type_traits>
@@ -61,53 +62,17 @@
 namespace kl {
 namespace {
 
-// Compile-time tuning knobs (defaults are the measured best on MI355X).
-#ifndef KL_DECODE_WAVES
-#define KL_DECODE_WAVES 4
-#endif
-#ifndef KL_DECODE_STAGES
-#define KL_DECODE_STAGES 0  // register pipeline depth; 0 picks per head_dim
-#endif
-#ifndef KL_DECODE_SPLIT_ISSUE
-#define KL_DECODE_SPLIT_ISSUE 0  // issue a block's K and V loads in two bursts
-#endif
-#ifndef KL_DECODE_WAVES_PER_EU
-#define KL_DECODE_WAVES_PER_EU 0  // occupancy floor for the register allocator; 0 picks per shape
-#endif
-#ifndef KL_DECODE_BALANCED_WG_PER_CU
-#define KL_DECODE_BALANCED_WG_PER_CU 1  // balanced-schedule workgroups per compute unit
-#endif
-#ifndef KL_DECODE_BALANCE_ALWAYS
-#define KL_DECODE_BALANCE_ALWAYS 0  // balanced schedule also when units fill the device
-#endif
-#ifndef KL_DECODE_MIN_PAGES
-#define KL_DECODE_MIN_PAGES 16  // fewest pages a planned uniform split takes
-#endif
-#ifndef KL_DECODE_BALANCED_MIN_PAGES
-#define KL_DECODE_BALANCED_MIN_PAGES 8  // fewest pages a balanced-schedule workgroup takes
-#endif
-#ifndef KL_DECODE_XCD_REMAP
-#define KL_DECODE_XCD_REMAP 0  // give each XCD a contiguous range of work units
-#endif
-#ifndef KL_DECODE_PAIRED
-#define KL_DECODE_PAIRED 1  // two adjacent KV heads per 8-wave workgroup where the pairs fill the device
-#endif
-#ifndef KL_DECODE_BALANCED_WAVES
-#define KL_DECODE_BALANCED_WAVES 4  // waves of a balanced-schedule workgroup (head_dim <= 128)
-#endif
-#ifndef KL_DECODE_FUSED_MERGE
-#define KL_DECODE_FUSED_MERGE 1  // the last segment of a split unit merges it (no merge kernel)
-#endif
-#ifndef KL_DECODE_KV_POLICY
-#define KL_DECODE_KV_POLICY kCachePolicyNT  // cache-policy bits of the K/V loads
-#endif
-
-constexpr int kWaves = KL_DECODE_WAVES;  // waves per workgroup
+// Tuning constants, each the measured best on MI355X.
+constexpr int kWaves = 4;  // waves per workgroup (a KV-head pair's workgroup has two sets)
 constexpr int kThreads = kWaves * 64;
 constexpr int kBlock = 16;     // tokens per MFMA block
 constexpr int kMaxPlannedSplits = 64;
-constexpr int kMinPagesPerSplit = KL_DECODE_MIN_PAGES;
-constexpr int kMinPagesPerBalancedWg = KL_DECODE_BALANCED_MIN_PAGES;
+constexpr int kMinPagesPerSplit = 16;      // fewest pages a planned uniform split takes
+constexpr int kMinPagesPerBalancedWg = 8;  // fewest pages a balanced-schedule workgroup takes
+// Cache policy of the K/V loads: streamed once, so non-temporal. Measured on
+// 32/8/128 fp16 B=64 ctx 4096: nt 173 us, nt with sc0 and/or sc1 172.5-173.7,
+// no policy bits 221.
+constexpr int kKvPolicy = kCachePolicyNT;
 // A batch with fewer units than 2 x CUs runs the balanced schedule in KV-head
 // pairs when every workgroup half streams at least kPairMinPages pages and no
 // pair unit is cut into more than kPairMaxSegments segments. Measured on
@@ -118,7 +83,7 @@ constexpr int kMinPagesPerBalancedWg = KL_DECODE_BALANCED_MIN_PAGES;
 constexpr int kPairMinPages = 128;
 constexpr int kPairMaxSegments = 16;
 // Full batches take the balanced schedule from this many block-table columns
-// on (see balance_override), as long as its workspace stays within
+// on (see make_plan), as long as its workspace stays within
 // kAutoBalanceMaxWorkspace (the no-allocation entry point's array).
 constexpr int kBalanceMinPages = 256;
 constexpr size_t kAutoBalanceMaxWorkspace = size_t{16} << 20;
@@ -170,18 +135,6 @@ struct Unit {
   int page_begin, page_end;
 };
 
-// Workgroups are dispatched to the 8 XCDs round-robin (workgroup i runs on
-// XCD i % 8). This bijection on [0, n) hands XCD x a contiguous range of
-// work ids instead of every 8th one.
-__device__ __forceinline__ int xcd_remap(int pid, int n) {
-  constexpr int kXcds = 8;
-  const int per = (n + kXcds - 1) / kXcds;
-  const int tall = n - (per - 1) * kXcds;  // XCDs that get `per` ids (1 .. 8)
-  const int xcd = pid % kXcds;
-  const int local = pid / kXcds;
-  return xcd < tall ? xcd * per + local : tall * per + (xcd - tall) * (per - 1) + local;
-}
-
 // The sequence length and this split's page range of a unit whose b and
 // split are set.
 __device__ __forceinline__ void unit_pages(const DecodeArgs& a, Unit& u) {
@@ -195,7 +148,7 @@ __device__ __forceinline__ void unit_pages(const DecodeArgs& a, Unit& u) {
 
 __device__ __forceinline__ Unit decode_unit(const DecodeArgs& a) {
   Unit u;
-  int idx = KL_DECODE_XCD_REMAP ? xcd_remap(blockIdx.x, gridDim.x) : static_cast<int>(blockIdx.x);
+  int idx = static_cast<int>(blockIdx.x);
   u.split = idx % a.num_splits;
   idx /= a.num_splits;
   u.hg = idx % a.head_groups;
@@ -309,7 +262,6 @@ struct MfmaLds {
 // balanced kernel needs more than its 256 registers and spills.
 template <int D, int NT>
 constexpr int mfma_stages() {
-  if (KL_DECODE_STAGES > 0) return KL_DECODE_STAGES;
   return D <= 64 ? (NT == 2 ? 4 : 6) : 2;
 }
 
@@ -319,7 +271,6 @@ constexpr int mfma_stages() {
 // spills. Single-tile kernels run best at the allocator's own choice.
 template <int D, int NT>
 constexpr int mfma_waves_per_eu() {
-  if (KL_DECODE_WAVES_PER_EU > 0) return KL_DECODE_WAVES_PER_EU;
   return NT == 2 ? 2 : 1;
 }
 
@@ -451,19 +402,13 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
            static_cast<int64_t>((blk - pidx * bpp) * kBlock) * a.token_stride + static_cast<int64_t>(u.kvh) * D;
   };
 
-  auto load_k = [&](int64_t base, u32x4 (&kf)[NL]) {
+  auto load_block = [&](int64_t base, u32x4 (&kf)[NL], u32x4 (&vf)[NL]) {
     const auto kr = make_rsrc(kc + base);
-#pragma unroll
-    for (int c = 0; c < NL; ++c) kf[c] = buffer_load16<KL_DECODE_KV_POLICY>(kr, kv_off[c]);
-  };
-  auto load_v = [&](int64_t base, u32x4 (&vf)[NL]) {
     const auto vr = make_rsrc(vc + base);
 #pragma unroll
-    for (int c = 0; c < NL; ++c) vf[c] = buffer_load16<KL_DECODE_KV_POLICY>(vr, kv_off[c]);
-  };
-  auto load_block = [&](int64_t base, u32x4 (&kf)[NL], u32x4 (&vf)[NL]) {
-    load_k(base, kf);
-    load_v(base, vf);
+    for (int c = 0; c < NL; ++c) kf[c] = buffer_load16<kKvPolicy>(kr, kv_off[c]);
+#pragma unroll
+    for (int c = 0; c < NL; ++c) vf[c] = buffer_load16<kKvPolicy>(vr, kv_off[c]);
   };
   // One 16-byte load's elements into a staging row as E: a plain store for a
   // 16-bit cache, decoded to two 16-byte chunks for FP8.
@@ -478,7 +423,7 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
     }
   };
 
-  auto process_block = [&](int i, const u32x4 (&kf)[NL], const u32x4 (&vf)[NL], auto&& mid) {
+  auto process_block = [&](int i, const u32x4 (&kf)[NL], const u32x4 (&vf)[NL]) {
     // Valid tokens in the block: >= 16 means all; <= 0 only for the padding
     // slots of the last pipeline round (i >= nblk).
     const int nvalid = i < nblk ? u.seq_len - (first + W * i) * kBlock : 0;
@@ -527,9 +472,6 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
       }
     }
 
-    // Issue the next loads (the caller's hook) between the two phases, so a
-    // wave's loads go out in two smaller bursts.
-    mid();
     // Stage V, rows past seq_len as zeros, for the transposed reads.
 #pragma unroll
     for (int c = 0; c < NL; ++c) {
@@ -563,13 +505,8 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
       for (int s = 0; s < NS; ++s) {
         const int i = base + s;
         const int64_t nb = next_base;
-#if KL_DECODE_SPLIT_ISSUE
-        load_k(nb, kb[(s + NS - 1) % NS]);
-        process_block(i, kb[s], vb[s], [&] { load_v(nb, vb[(s + NS - 1) % NS]); });
-#else
         load_block(nb, kb[(s + NS - 1) % NS], vb[(s + NS - 1) % NS]);
-        process_block(i, kb[s], vb[s], [] {});
-#endif
+        process_block(i, kb[s], vb[s]);
         next_base = block_base(min(i + NS, nblk - 1));
       }
     }
@@ -1076,16 +1013,11 @@ __device__ __forceinline__ Start schedule_start(const DecodeArgs& a, int units_p
   return s;
 }
 
-// Waves of a balanced-schedule workgroup (one workgroup per CU). Measured on
-// MI355X, 8 waves instead of 4 were slower at batch 1-16 (B=1 ctx 512: 15.6
-// vs 12.9 us, B=8 ctx 512: 18.0 vs 14.4 us) and equal on long contexts: these
-// launches are bound by latency chains and the cross-wave merge, not by the
-// loads in flight. head_dim 256 always takes 4 (8 waves cap a wave at 256
-// registers, below what its segment needs).
-template <int D>
-constexpr int balanced_waves() {
-  return D <= 128 ? KL_DECODE_BALANCED_WAVES : kWaves;
-}
+// A balanced-schedule workgroup (one per CU, or one per CU and KV-head pair)
+// has kWaves waves per KV head. Measured on MI355X, 8 waves per head instead
+// of 4 were slower at batch 1-16 (B=1 ctx 512: 15.6 vs 12.9 us, B=8 ctx 512:
+// 18.0 vs 14.4 us) and equal on long contexts: these launches are bound by
+// latency chains and the cross-wave merge, not by the loads in flight.
 
 // The list workgroup w that hardware workgroup i runs, in KV-head pairs.
 // Workgroups are dealt to the XCDs round robin (i % 8). When each pair unit
@@ -1116,9 +1048,9 @@ __device__ __forceinline__ int paired_list_wg(const DecodeArgs& a, int units_per
 // of every token row, as in decode_mfma_paired_kernel). Half h of segment
 // (list workgroup w, list unit u) owns partial slot (w + u) * 2 + h.
 template <typename E, typename KVF, int D, int NT, int PAIR>
-__global__ void __launch_bounds__(PAIR * balanced_waves<D>() * 64, (mfma_waves_per_eu<D, NT>()))
+__global__ void __launch_bounds__(PAIR * kThreads, (mfma_waves_per_eu<D, NT>()))
     decode_mfma_balanced_kernel(const DecodeArgs a) {
-  constexpr int W = balanced_waves<D>();
+  constexpr int W = kWaves;
   __shared__ __attribute__((aligned(16))) char lds[PAIR * MfmaLds<D, NT, W>::kBytes];
   __shared__ int s_last[PAIR];
   // A compile-time 0 with PAIR == 1, so the LDS base stays a constant.
@@ -1729,45 +1661,54 @@ bool mfma_path(kl_dtype dtype, int head_dim, int page_size) {
          (head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256);
 }
 
-// KL_DECODE_FORCE_VALU=1 in the environment (read on every call) sends 16-bit
-// decode to the VALU kernel, so benchmarks can time the two paths on the same
-// shapes; the FP8 and cascade entry points ignore it.
-bool valu_forced() {
-  const char* v = std::getenv("KL_DECODE_FORCE_VALU");
-  return v != nullptr && v[0] == '1';
+// Switches for A/B measurements and tests; unset, the library behaves as
+// planned below. They are read from the environment once per process, at
+// the first call that needs them, and again by
+// kl_paged_decode_reload_options():
+//   KL_DECODE_FORCE_VALU=1        16-bit decode on the VALU kernel, so the
+//                                 benchmarks can time both paths on the same
+//                                 shapes (the FP8 and cascade entry points
+//                                 ignore it)
+//   KL_DECODE_PAIRED=0            no paired (two KV heads) workgroups
+//   KL_DECODE_BALANCE_ALWAYS=1|0  full batches always balanced | always
+//                                 uniform (the default chooses by table
+//                                 length; see make_plan)
+//   KL_DECODE_FUSED_MERGE=0       split decodes merge in a separate launch
+struct Options {
+  static constexpr unsigned kLoaded = 1, kForceValu = 2, kNoPairs = 4, kNoFusedMerge = 8, kBalanceAlways = 16,
+                            kBalanceNever = 32;
+  unsigned bits = kLoaded;
+  bool force_valu() const { return (bits & kForceValu) != 0; }
+  bool pairing() const { return (bits & kNoPairs) == 0; }
+  bool fused_merge() const { return (bits & kNoFusedMerge) == 0; }
+  // Full-batch schedule: 1 balanced, 0 uniform, -1 by table length.
+  int balance() const { return (bits & kBalanceAlways) ? 1 : (bits & kBalanceNever) ? 0 : -1; }
+};
+
+std::atomic<unsigned> g_option_bits{0};  // 0: not read yet
+
+unsigned read_option_bits() {
+  auto starts = [](const char* name, char c) {
+    const char* v = std::getenv(name);
+    return v != nullptr && v[0] == c;
+  };
+  unsigned bits = Options::kLoaded;
+  if (starts("KL_DECODE_FORCE_VALU", '1')) bits |= Options::kForceValu;
+  if (starts("KL_DECODE_PAIRED", '0')) bits |= Options::kNoPairs;
+  if (starts("KL_DECODE_FUSED_MERGE", '0')) bits |= Options::kNoFusedMerge;
+  if (starts("KL_DECODE_BALANCE_ALWAYS", '1')) bits |= Options::kBalanceAlways;
+  if (starts("KL_DECODE_BALANCE_ALWAYS", '0')) bits |= Options::kBalanceNever;
+  return bits;
 }
 
-// KL_DECODE_PAIRED=0 turns paired workgroups off (for A/B measurements).
-bool pairing_enabled() {
-  if (!KL_DECODE_PAIRED) return false;
-  const char* v = std::getenv("KL_DECODE_PAIRED");
-  return v == nullptr || v[0] != '0';
-}
-
-// The planner's choice for fp16/bf16 batches whose units fill the device
-// (units >= CUs) is the balanced schedule when the block table is long
-// (kBalanceMinPages or more columns) and uniform splits otherwise. The
-// planner cannot see seq_lens, and with uniform splits one long sequence
-// among short ones sets the time: measured on MI355X (events, us, same
-// tensors alternating), one 65,536-token sequence among 63 of 2,048 tokens
-// 1,231 (uniform) vs 142 (balanced), ragged U[1, 8192] B=64 228 vs 207. On an
-// even batch the balanced schedule gives every workgroup the same single unit
-// and costs only its start: 163.4 vs 164.6 (32/8/128 fp16 B=64 ctx 4096),
-// but on short tables that start weighs more (B=32 ctx 512 19.0 vs 19.9,
-// B=128 ctx 2048 169.0 vs 174.2) while the worst skew costs less.
-// KL_DECODE_BALANCE_ALWAYS in the environment (read on every call) overrides
-// the choice for full batches: 1 always balanced, 0 always uniform.
-int balance_override() {
-  const char* v = std::getenv("KL_DECODE_BALANCE_ALWAYS");
-  if (v != nullptr && (v[0] == '0' || v[0] == '1')) return v[0] == '1' ? 1 : 0;
-  return KL_DECODE_BALANCE_ALWAYS != 0 ? 1 : -1;
-}
-
-// KL_DECODE_FUSED_MERGE=0 sends every split decode to the merge kernels.
-bool fused_merge_enabled() {
-  if (!KL_DECODE_FUSED_MERGE) return false;
-  const char* v = std::getenv("KL_DECODE_FUSED_MERGE");
-  return v == nullptr || v[0] != '0';
+Options options() {
+  Options o;
+  o.bits = g_option_bits.load(std::memory_order_relaxed);
+  if (o.bits == 0) {
+    o.bits = read_option_bits();
+    g_option_bits.store(o.bits, std::memory_order_relaxed);
+  }
+  return o;
 }
 
 // The arrival-counter region for a fused call on `stream` (current device),
@@ -1814,6 +1755,21 @@ uint32_t* arrival_region(hipStream_t stream) {
     (void)hipGetLastError();
     return nullptr;
   }
+  const unsigned long long key = capturing ? capture : 0;
+  // Most calls repeat the calling thread's last (device, stream, capture):
+  // regions are never handed back, so its answer still holds.
+  struct Last {
+    int dev = -1;
+    hipStream_t stream = nullptr;
+    unsigned long long key = 0;
+    bool capturing = false;
+    uint32_t* region = nullptr;
+  };
+  thread_local Last last;
+  if (last.region != nullptr && last.dev == dev && last.stream == stream && last.key == key &&
+      last.capturing == capturing) {
+    return last.region;
+  }
   std::lock_guard<std::mutex> lock(mu);
   Device& d = devices[dev];
   if (!d.located) {
@@ -1832,11 +1788,12 @@ uint32_t* arrival_region(hipStream_t stream) {
   int& taken = capturing ? d.captured_taken : d.eager_taken;
   const int size = capturing ? kCaptureRegions : kStreamRegions;
   const int first = capturing ? kStreamRegions : 0;  // region index of the pool's first entry
-  const unsigned long long key = capturing ? capture : 0;
+  auto remember = [&](int i) {
+    last = Last{dev, stream, key, capturing, d.base + static_cast<size_t>(first + i) * kArrivalCounters};
+    return last.region;
+  };
   for (int i = 0; i < taken; ++i) {
-    if (pool[i].stream == stream && pool[i].capture == key) {
-      return d.base + static_cast<size_t>(first + i) * kArrivalCounters;
-    }
+    if (pool[i].stream == stream && pool[i].capture == key) return remember(i);
   }
   if (taken == size) {
     bool& warned = capturing ? d.warned_captured : d.warned_eager;
@@ -1850,7 +1807,7 @@ uint32_t* arrival_region(hipStream_t stream) {
     return nullptr;
   }
   pool[taken] = Owner{stream, key};
-  return d.base + static_cast<size_t>(first + taken++) * kArrivalCounters;
+  return remember(taken++);
 }
 
 // How the last decode launch on this thread combined split units
@@ -1860,7 +1817,7 @@ thread_local int g_last_merge = KL_MERGE_NONE;
 // Arrival counters for a split decode of `units` units with up to
 // heads_per_wg heads each on the MFMA path, or null for the merge kernel.
 uint32_t* fused_merge_counters(const DecodeArgs& a, int64_t units, hipStream_t stream) {
-  if (!fused_merge_enabled() || units > kArrivalCounters || a.heads_per_wg > kFusedMergeMaxHeads) return nullptr;
+  if (!options().fused_merge() || units > kArrivalCounters || a.heads_per_wg > kFusedMergeMaxHeads) return nullptr;
   if (a.q_fold != a.group || a.force_partial) return nullptr;  // cascade passes keep their own merge
   // Segments per unit: the split count, or for the balanced schedule the
   // workgroups per list unit on even lengths.
@@ -1912,16 +1869,15 @@ struct Plan {
   size_t ws_bytes;
 };
 
-constexpr int kBalancedWgPerCu = KL_DECODE_BALANCED_WG_PER_CU;
-
 constexpr size_t kAlign = 256;
 size_t align_up(size_t n) { return (n + kAlign - 1) / kAlign * kAlign; }
 
 // partials: a pass of cascade decode, which always takes uniform splits and
 // writes fp32 partials (workspace sized for them even with one split).
 // use_mfma false: plan for the VALU kernel even where the MFMA one could run.
-int make_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads, int head_dim, int page_size,
-              int max_pages, int num_splits, int cu_count, Plan* p, bool partials = false, bool use_mfma = true) {
+int make_plan(const Options& opt, kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+              int page_size, int max_pages, int num_splits, int cu_count, Plan* p, bool partials = false,
+              bool use_mfma = true) {
   if (batch < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 || max_pages < 0) {
     return fail(KL_ERR_INVALID_ARGUMENT, "batch, heads, head_dim, page_size and max_pages must be positive");
   }
@@ -1953,9 +1909,20 @@ int make_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads, int 
   const int64_t pair_units = units / 2;
   const bool long_pairs = pair_units * pages >= static_cast<int64_t>(cus) * kPairMinPages &&
                           pair_units * kPairMaxSegments >= cus;
-  const bool pairable = mfma && !partials && pairing_enabled() && num_kv_heads % 2 == 0 && head_dim <= 128 &&
+  const bool pairable = mfma && !partials && opt.pairing() && num_kv_heads % 2 == 0 && head_dim <= 128 &&
                         p->heads_per_wg <= 16 && (units >= 2 * static_cast<int64_t>(cus) || long_pairs);
-  const int full_batch_choice = balance_override();  // 1 balanced, 0 uniform, -1 by table length
+  // For batches whose units fill the device (units >= CUs) the choice is the
+  // balanced schedule when the block table is long (kBalanceMinPages or more
+  // columns) and uniform splits otherwise. The planner cannot see seq_lens,
+  // and with uniform splits one long sequence among short ones sets the time:
+  // measured on MI355X (events, us, same tensors alternating), one
+  // 65,536-token sequence among 63 of 2,048 tokens 1,231 (uniform) vs 142
+  // (balanced), ragged U[1, 8192] B=64 228 vs 207. On an even batch the
+  // balanced schedule gives every workgroup the same single unit and costs
+  // only its start: 163.4 vs 164.6 (32/8/128 fp16 B=64 ctx 4096), but on
+  // short tables that start weighs more (B=32 ctx 512 19.0 vs 19.9, B=128
+  // ctx 2048 169.0 vs 174.2) while the worst skew costs less.
+  const int full_batch_choice = opt.balance();  // 1 balanced, 0 uniform, -1 by table length
   const bool requested = num_splits == KL_SPLITS_BALANCED;
   const bool automatic =
       num_splits == 0 && (units < cus || (full_batch_choice < 0 ? pages >= kBalanceMinPages : full_batch_choice == 1));
@@ -1968,7 +1935,7 @@ int make_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads, int 
     // Paired: one 8-wave workgroup per CU is the register budget, so more
     // workgroups would run in rounds, each paying the schedule's start.
     const int64_t floor_wgs =
-        pair_balanced ? static_cast<int64_t>(cus) : std::max<int64_t>(static_cast<int64_t>(cus) * kBalancedWgPerCu, lunits);
+        pair_balanced ? static_cast<int64_t>(cus) : std::max<int64_t>(cus, lunits);
     const int64_t grid =
         std::max<int64_t>(1, std::min<int64_t>({cdiv(upper, kMinPagesPerBalancedWg), floor_wgs, 0x7fffffffLL}));
     p->grid = static_cast<int>(grid);
@@ -2005,7 +1972,7 @@ int make_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads, int 
   // Two adjacent KV heads per 8-wave workgroup when the pairs alone give
   // every CU a workgroup (one 8-wave workgroup per CU is the register budget)
   // and the 4-wave kernel fits two waves per SIMD (head_dim <= 128).
-  p->paired = mfma && pairing_enabled() && num_kv_heads % 2 == 0 && head_dim <= 128 && units * s / 2 >= cus;
+  p->paired = mfma && opt.pairing() && num_kv_heads % 2 == 0 && head_dim <= 128 && units * s / 2 >= cus;
   if (s > 1 || partials) {
     const size_t rows = static_cast<size_t>(batch) * num_q_heads * s;
     p->o_bytes = align_up(rows * head_dim * sizeof(float));
@@ -2015,6 +1982,36 @@ int make_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads, int 
     p->ws_bytes = 0;
   }
   return ok();
+}
+
+// The last decode plan made on this thread and the arguments it was made
+// for: a caller that sizes the workspace with kl_paged_decode_plan and then
+// launches with the same arguments (the PyTorch operator does) plans once.
+struct PlanMemo {
+  static constexpr int kKeyLen = 11;
+  int key[kKeyLen] = {};
+  Plan plan{};
+  bool valid = false;
+};
+thread_local PlanMemo g_plan_memo;
+
+int decode_plan(const Options& opt, kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                int page_size, int max_pages, int num_splits, int cu_count, bool use_mfma, Plan* p) {
+  const int key[PlanMemo::kKeyLen] = {static_cast<int>(opt.bits), static_cast<int>(dtype), batch, num_q_heads,
+                                      num_kv_heads, head_dim, page_size, max_pages, num_splits, cu_count,
+                                      use_mfma ? 1 : 0};
+  PlanMemo& m = g_plan_memo;
+  if (m.valid && std::equal(key, key + PlanMemo::kKeyLen, m.key)) {
+    *p = m.plan;
+    return ok();
+  }
+  const int st = make_plan(opt, dtype, batch, num_q_heads, num_kv_heads, head_dim, page_size, max_pages, num_splits,
+                           cu_count, p, false, use_mfma);
+  if (st != KL_OK) return st;
+  std::copy(key, key + PlanMemo::kKeyLen, m.key);
+  m.plan = *p;
+  m.valid = true;
+  return st;
 }
 
 template <int N>
@@ -2117,12 +2114,12 @@ int launch_balanced(DecodeArgs a, int head_dim, hipStream_t stream) {
         // One head tile and head_dim <= 128: beyond that the segment needs
         // more than the 256 registers per lane of an 8-wave workgroup.
         if constexpr (D <= 128 && NT == 1) {
-          decode_mfma_balanced_kernel<E, KVF, D, NT, 2><<<grid, 2 * balanced_waves<D>() * 64, 0, stream>>>(a);
+          decode_mfma_balanced_kernel<E, KVF, D, NT, 2><<<grid, 2 * kThreads, 0, stream>>>(a);
         } else {
           return fail(KL_ERR_UNSUPPORTED, "paired balanced decode needs head_dim <= 128 and <= 16 heads per workgroup");
         }
       } else {
-        decode_mfma_balanced_kernel<E, KVF, D, NT, 1><<<grid, balanced_waves<D>() * 64, 0, stream>>>(a);
+        decode_mfma_balanced_kernel<E, KVF, D, NT, 1><<<grid, kThreads, 0, stream>>>(a);
       }
       return KL_OK;
     } else {
@@ -2180,9 +2177,10 @@ extern "C" int kl_paged_decode_plan(kl_dtype dtype, int batch, int num_q_heads, 
                                     int* out_num_splits, size_t* out_workspace) {
   using namespace kl;
   if (cu_count <= 0) cu_count = current_cu_count();
+  const Options opt = options();
   Plan p;
-  const int st = make_plan(dtype, batch, num_q_heads, num_kv_heads, head_dim, page_size, max_pages, num_splits,
-                           cu_count, &p, false, !valu_forced());
+  const int st = decode_plan(opt, dtype, batch, num_q_heads, num_kv_heads, head_dim, page_size, max_pages,
+                             num_splits, cu_count, !opt.force_valu(), &p);
   if (st != KL_OK) return st;
   if (out_num_splits) *out_num_splits = p.num_splits;
   if (out_workspace) *out_workspace = p.ws_bytes;
@@ -2210,10 +2208,11 @@ int decode_entry(kl_dtype dtype, bool kv8, void* out, const void* q, const void*
     }
     if (!k_scale || !v_scale) return fail(KL_ERR_INVALID_ARGUMENT, "k_scale and v_scale must be non-null");
   }
-  const bool use_mfma = kv8 || !valu_forced();
+  const Options opt = options();
+  const bool use_mfma = kv8 || !opt.force_valu();
   Plan p;
-  int st = make_plan(dtype, batch, num_q_heads, num_kv_heads, head_dim, page_size, max_pages, num_splits,
-                     current_cu_count(), &p, false, use_mfma);
+  int st = decode_plan(opt, dtype, batch, num_q_heads, num_kv_heads, head_dim, page_size, max_pages, num_splits,
+                       current_cu_count(), use_mfma, &p);
   if (st != KL_OK) return st;
   if (!out || !q || !k_cache || !v_cache || !block_table || !seq_lens) {
     return fail(KL_ERR_INVALID_ARGUMENT, "out, q, k_cache, v_cache, block_table and seq_lens must be non-null");
@@ -2296,6 +2295,11 @@ extern "C" int kl_paged_decode_attention(kl_dtype dtype, void* out, const void* 
 }
 
 extern "C" int kl_paged_decode_last_merge(void) { return kl::g_last_merge; }
+
+extern "C" int kl_paged_decode_reload_options(void) {
+  kl::g_option_bits.store(kl::read_option_bits(), std::memory_order_relaxed);
+  return kl::ok();
+}
 
 // --------------------------------------------- no-allocation decode entry point
 //
@@ -2419,11 +2423,12 @@ int cascade_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_heads, i
   }
   const int64_t folded = static_cast<int64_t>(std::max(batch, 1)) * (num_q_heads / num_kv_heads);
   if (folded * num_kv_heads > 0x7fffffffLL) return fail(KL_ERR_UNSUPPORTED, "batch * num_q_heads too large");
-  int st = make_plan(dtype, 1, static_cast<int>(folded * num_kv_heads), num_kv_heads, head_dim, page_size,
+  const Options opt = options();
+  int st = make_plan(opt, dtype, 1, static_cast<int>(folded * num_kv_heads), num_kv_heads, head_dim, page_size,
                      std::max(prefix_pages, 1), 0, cu_count, &cp->pre, true);
   if (st != KL_OK) return st;
-  st = make_plan(dtype, std::max(batch, 1), num_q_heads, num_kv_heads, head_dim, page_size, std::max(max_pages, 1),
-                 0, cu_count, &cp->suf, true);
+  st = make_plan(opt, dtype, std::max(batch, 1), num_q_heads, num_kv_heads, head_dim, page_size,
+                 std::max(max_pages, 1), 0, cu_count, &cp->suf, true);
   if (st != KL_OK) return st;
   cp->pre_bytes = align_up(cp->pre.ws_bytes);
   cp->ws_bytes = cp->pre_bytes + cp->suf.ws_bytes;

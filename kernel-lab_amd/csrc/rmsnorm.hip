@@ -31,21 +31,16 @@ struct alignas(sizeof(S) * N) Pack {
 
 // Pack loads and stores keep the default cache policy: measured on MI355X for
 // this read/write mix, non-temporal stores lose ~10% of HBM bandwidth and
-// non-temporal loads ~7%. KL_RMS_LOAD_POLICY = 1 selects streaming loads.
-#ifndef KL_RMS_LOAD_POLICY
-#define KL_RMS_LOAD_POLICY 0
-#endif
-#ifndef KL_RMS_PACKS_PER_THREAD
-#define KL_RMS_PACKS_PER_THREAD 2
-#endif
+// non-temporal loads ~7%.
 template <typename S, int N>
 __device__ __forceinline__ Pack<S, N> load_pack(const Pack<S, N>* p) {
-  if constexpr (sizeof(Pack<S, N>) == 16 && KL_RMS_LOAD_POLICY == 1) {
-    return __builtin_bit_cast(Pack<S, N>, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p)));
-  } else {
-    return *p;
-  }
+  return *p;
 }
+
+// Packs per thread the launch aims for (threads = packs / 2, in whole waves,
+// 64..1024): measured on MI355X at hidden 8192 bf16, one, four and eight
+// 16-byte packs per tensor per thread were slower than two.
+constexpr int kPacksPerThread = 2;
 
 template <typename S, int N>
 __device__ __forceinline__ void store_pack(Pack<S, N>* p, const Pack<S, N>& v) {
@@ -112,12 +107,19 @@ __global__ void __launch_bounds__(kMaxThreads)
     a[k] = load_pack(xr + idx[k]);
     if constexpr (HAS_RES) b[k] = load_pack(rr + idx[k]);
   }
-  // Weights are loaded before the reduction so their latency overlaps it.
+  // Weights are loaded before the reduction so their latency overlaps it,
+  // except at NPACK = 8, where their registers beside x's and the residual's
+  // would exceed the 128 a lane has at 1024 threads and spill.
+  constexpr bool kEarlyWeights = NPACK <= 4;
   P w[NPACK];
+  if constexpr (kEarlyWeights) {
 #pragma unroll
-  for (int k = 0; k < NPACK; ++k) w[k] = wr[idx[k]];
+    for (int k = 0; k < NPACK; ++k) w[k] = wr[idx[k]];
+  }
 
-  float f[NPACK][VEC];
+  // The rounded sum stays packed across the block reduction and is widened
+  // again for the output: keeping an fp32 copy live as well would need
+  // NPACK * VEC more registers and spill at NPACK = 8.
   P s[NPACK];
   float sum_sq = 0.0f;
 #pragma unroll
@@ -131,8 +133,8 @@ __global__ void __launch_bounds__(kMaxThreads)
     float part = 0.0f;
 #pragma unroll
     for (int j = 0; j < VEC; ++j) {
-      f[k][j] = E::to_f32(s[k].v[j]);
-      part += f[k][j] * f[k][j];
+      const float f = E::to_f32(s[k].v[j]);
+      part += f * f;
     }
     sum_sq += valid[k] ? part : 0.0f;
   }
@@ -143,13 +145,27 @@ __global__ void __launch_bounds__(kMaxThreads)
     }
   }
 
+  if constexpr (!kEarlyWeights) {
+#pragma unroll
+    for (int k = 0; k < NPACK; ++k) w[k] = wr[idx[k]];
+  }
   const float rstd = inv_rms(block_sum(sum_sq, scratch), hidden, eps);
+  if constexpr (!kEarlyWeights && sizeof(P) == 16) {
+    // Keep the sums packed until here: widened ahead of the reduction (the
+    // compiler's choice otherwise) they would take twice the registers.
+#pragma unroll
+    for (int k = 0; k < NPACK; ++k) {
+      u32x4 r = __builtin_bit_cast(u32x4, s[k]);
+      asm volatile("" : "+v"(r));
+      s[k] = __builtin_bit_cast(P, r);
+    }
+  }
 
 #pragma unroll
   for (int k = 0; k < NPACK; ++k) {
     P o;
 #pragma unroll
-    for (int j = 0; j < VEC; ++j) o.v[j] = E::from_f32((f[k][j] * rstd) * E::to_f32(w[k].v[j]));
+    for (int j = 0; j < VEC; ++j) o.v[j] = E::from_f32((E::to_f32(s[k].v[j]) * rstd) * E::to_f32(w[k].v[j]));
     if (valid[k]) store_pack(orow + idx[k], o);
   }
 }
@@ -241,9 +257,9 @@ int launch_vec(void* out, const void* x, void* res, const void* w, int64_t rows,
   auto* r = static_cast<S*>(res);
   auto* wi = static_cast<const S*>(w);
   const int packs = hidden / VEC;
-  // About KL_RMS_PACKS_PER_THREAD packs per thread, in whole waves, 64..1024 threads.
+  // About kPacksPerThread packs per thread, in whole waves, 64..1024 threads.
   int threads = static_cast<int>(std::min<int64_t>(
-      kMaxThreads, std::max<int64_t>(64, cdiv(cdiv(packs, KL_RMS_PACKS_PER_THREAD), 64) * 64)));
+      kMaxThreads, std::max<int64_t>(64, cdiv(cdiv(packs, kPacksPerThread), 64) * 64)));
   const int npack = static_cast<int>(cdiv(packs, threads));
   const dim3 grid(static_cast<unsigned>(rows));
   if (npack <= 1) {

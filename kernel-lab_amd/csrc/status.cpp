@@ -1,8 +1,7 @@
 // Status strings, per-thread error detail and device queries for the C-ABI.
+#include <atomic>
 #include <cstdio>
 #include <cstring>
-#include <mutex>
-#include <vector>
 
 #include "kl_internal.h"
 
@@ -36,20 +35,22 @@ int check_launch(const char* what) {
 }
 
 int current_cu_count() {
-  static std::mutex mu;
-  static std::vector<int> cache;
+  // One slot per device, filled on first use; a racing second fill stores the
+  // same value, so no lock is needed.
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cache[kMaxDevices];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
-  std::lock_guard<std::mutex> lock(mu);
-  if (static_cast<size_t>(dev) >= cache.size()) cache.resize(dev + 1, 0);
-  if (cache[dev] == 0) {
+  if (dev >= kMaxDevices) {
     int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
-      return 0;
-    }
-    cache[dev] = cus;
+    return hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess ? cus : 0;
   }
-  return cache[dev];
+  int cus = cache[dev].load(std::memory_order_relaxed);
+  if (cus == 0) {
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cache[dev].store(cus, std::memory_order_relaxed);
+  }
+  return cus;
 }
 
 }  // namespace kl

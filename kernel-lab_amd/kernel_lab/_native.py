@@ -14,8 +14,11 @@ There is no fallback. If the libraries are missing, ``available()`` is False,
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
+import os
 from pathlib import Path
+from typing import Iterator
 
 import torch
 
@@ -44,6 +47,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i64, _i32, _f32, _vp, _sz, _vp],
     ),
     "kl_paged_decode_last_merge": (_i32, []),
+    "kl_paged_decode_reload_options": (_i32, []),
     "kl_paged_decode_attention_noalloc": (
         _i32,
         [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i64, _i32, _f32, _i32, _vp],
@@ -119,3 +123,26 @@ def last_error() -> str:
 
 def status_string(status: int) -> str:
     return core().kl_status_string(status).decode()
+
+
+@contextlib.contextmanager
+def decode_switches(**values: str) -> Iterator[None]:
+    """Sets the library's decode switches for the block: each keyword names one
+    ``KL_DECODE_<NAME>`` environment variable (``paired="0"``,
+    ``force_valu="1"``, ``fused_merge="0"``, ``balance_always="1"``). The
+    library reads them once per process, so it is told to re-read them on entry
+    and again on exit, after the previous values are restored."""
+    names = {f"KL_DECODE_{key.upper()}": value for key, value in values.items()}
+    saved = {name: os.environ.get(name) for name in names}
+    lib = core()
+    try:
+        os.environ.update(names)
+        lib.kl_paged_decode_reload_options()
+        yield
+    finally:
+        for name, value in saved.items():
+            if value is None:
+                os.environ.pop(name, None)
+            else:
+                os.environ[name] = value
+        lib.kl_paged_decode_reload_options()

@@ -37,7 +37,6 @@ from __future__ import annotations
 
 import argparse
 import json
-import os
 import sys
 from collections.abc import Callable
 from dataclasses import asdict, dataclass
@@ -45,7 +44,7 @@ from pathlib import Path
 
 import torch
 
-from kernel_lab import ops
+from kernel_lab import _native, ops
 from kernel_lab.bench.roofline import GPUPeak, Work, decode_attention_work, lookup, rms_norm_work
 from kernel_lab.kv_cache import device_decode_problem, quantize_fp8, random_cascade_problem
 
@@ -285,23 +284,16 @@ def decode_cases(dtype: torch.dtype) -> list[tuple[str, list[int], int, int, tor
 
 
 def _forced_valu(fn: Callable[[], torch.Tensor]) -> torch.Tensor:
-    """Runs fn with the library's 16-bit decode sent to its VALU kernel
-    (KL_DECODE_FORCE_VALU, read by the library on every call)."""
-    os.environ["KL_DECODE_FORCE_VALU"] = "1"
-    try:
+    """Runs fn with the library's 16-bit decode sent to its VALU kernel."""
+    with _native.decode_switches(force_valu="1"):
         return fn()
-    finally:
-        del os.environ["KL_DECODE_FORCE_VALU"]
 
 
 def _unpaired(fn: Callable[[], torch.Tensor]) -> torch.Tensor:
     """Runs fn with paired workgroups (two adjacent KV heads per 8-wave
-    workgroup) switched off (KL_DECODE_PAIRED=0, read on every call)."""
-    os.environ["KL_DECODE_PAIRED"] = "0"
-    try:
+    workgroup) switched off."""
+    with _native.decode_switches(paired="0"):
         return fn()
-    finally:
-        del os.environ["KL_DECODE_PAIRED"]
 
 
 def decode_suite(

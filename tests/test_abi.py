@@ -120,13 +120,12 @@ def test_planner_balances_uneven_batches_by_default(batch, hkv, max_pages, balan
 
 
 @pytest.mark.parametrize(("batch", "hkv", "max_pages"), [(64, 8, 256), (32, 8, 256), (128, 8, 64), (64, 1, 512)])
-def test_balanced_planner_on_request(monkeypatch, batch, hkv, max_pages):
+def test_balanced_planner_on_request(batch, hkv, max_pages):
     """KL_DECODE_BALANCE_ALWAYS=1 gives every fp16/bf16 batch the balanced
-    schedule (read on every call). With an even KV head count and units >=
-    2 x CUs the list runs in KV-head pairs (one 8-wave workgroup per CU), with
-    a partial slot per half."""
-    monkeypatch.setenv("KL_DECODE_BALANCE_ALWAYS", "1")
-    splits, ws = ops.plan_decode(torch.float16, batch, hkv * 4, hkv, 128, 16, max_pages, 0, 256)
+    schedule. With an even KV head count and units >= 2 x CUs the list runs in
+    KV-head pairs (one 8-wave workgroup per CU), with a partial slot per half."""
+    with _native.decode_switches(balance_always="1"):
+        splits, ws = ops.plan_decode(torch.float16, batch, hkv * 4, hkv, 128, 16, max_pages, 0, 256)
     units = batch * hkv
     long_pairs = units // 2 * max_pages >= 256 * 128 and units // 2 * 16 >= 256
     paired = hkv % 2 == 0 and (units >= 512 or long_pairs)
@@ -135,8 +134,8 @@ def test_balanced_planner_on_request(monkeypatch, batch, hkv, max_pages):
     grid = min(floor, -(-lunits * max_pages // 8))
     slots = (grid + lunits) * (2 if paired else 1)
     assert splits == 0 and ws >= slots * 4 * (128 + 1) * 4
-    monkeypatch.setenv("KL_DECODE_BALANCE_ALWAYS", "0")
-    uniform = ops.plan_decode(torch.float16, batch, hkv * 4, hkv, 128, 16, max_pages, 0, 256)[0]
+    with _native.decode_switches(balance_always="0"):
+        uniform = ops.plan_decode(torch.float16, batch, hkv * 4, hkv, 128, 16, max_pages, 0, 256)[0]
     assert uniform >= 1 if units >= 256 else uniform == 0  # fewer units than CUs: balanced regardless
 
 
@@ -227,3 +226,32 @@ def test_planner_choices_fit_the_no_allocation_array():
                         if ws.value > worst[0]:
                             worst = (ws.value, (code, batch, hq, hkv, d, max_pages))
     assert 0 < worst[0] <= 16 << 20, worst
+
+
+def test_switches_are_read_once_and_on_reload(monkeypatch):
+    """The library reads its KL_DECODE_* switches once per process: a change to
+    the environment alone leaves the plan as it was (the last plan is also
+    remembered per thread, and must not outlive the switches), and
+    kl_paged_decode_reload_options() applies it."""
+    args = (torch.float16, 64, 32, 8, 128, 16, 256, 0, 256)  # full batch, 256 pages: balanced
+    assert ops.plan_decode(*args)[0] == 0
+    monkeypatch.setenv("KL_DECODE_BALANCE_ALWAYS", "0")
+    assert ops.plan_decode(*args)[0] == 0, "the environment was re-read without a reload"
+    lib = _native.core()
+    try:
+        assert lib.kl_paged_decode_reload_options() == 0
+        assert ops.plan_decode(*args)[0] == 1
+    finally:
+        monkeypatch.delenv("KL_DECODE_BALANCE_ALWAYS")
+        lib.kl_paged_decode_reload_options()
+    assert ops.plan_decode(*args)[0] == 0
+
+
+def test_remembered_plan_follows_its_arguments():
+    """Alternating two shapes returns each one's own plan every time."""
+    a = (torch.float16, 64, 32, 8, 128, 16, 256, 0, 256)
+    b = (torch.float16, 8, 32, 8, 128, 16, 32, 0, 256)
+    first = ops.plan_decode(*a), ops.plan_decode(*b)
+    for _ in range(3):
+        assert (ops.plan_decode(*a), ops.plan_decode(*b)) == first
+    assert first[0] != first[1]

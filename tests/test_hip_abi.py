@@ -101,7 +101,7 @@ def test_ops_work_under_torch_compile(gpu_ops):
     torch.testing.assert_close(y.cpu(), ref_y, **tolerance(torch.float16))
 
 
-def test_balanced_request_reaches_the_planner_on_full_batches(gpu_ops, monkeypatch):
+def test_balanced_request_reaches_the_planner_on_full_batches(gpu_ops):
     """64 sequences x 8 KV heads fill the device twice over. With
     KL_DECODE_BALANCE_ALWAYS=1 the planner's own choice is the balanced
     schedule in KV-head pairs (a workspace, 0 splits); by default (and with
@@ -121,11 +121,11 @@ def test_balanced_request_reaches_the_planner_on_full_batches(gpu_ops, monkeypat
         return splits.value, ws.value
 
     assert plan(0) == (1, 0)
-    monkeypatch.setenv("KL_DECODE_BALANCE_ALWAYS", "1")
-    balanced = plan(0)
+    with _native.decode_switches(balance_always="1"):
+        balanced = plan(0)
     assert balanced[0] == 0 and balanced[1] > 0
-    monkeypatch.setenv("KL_DECODE_BALANCE_ALWAYS", "0")
-    sizes = {0: plan(0), -1: plan(-1)}
+    with _native.decode_switches(balance_always="0"):
+        sizes = {0: plan(0), -1: plan(-1)}
     assert sizes[0] == (1, 0) and sizes[-1] == balanced
     out = torch.empty_like(q)
     args = [code, out.data_ptr(), q.data_ptr(), kv.k_cache.data_ptr(), kv.v_cache.data_ptr(), kv.block_table.data_ptr(),

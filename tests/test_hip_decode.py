@@ -17,6 +17,7 @@ import numpy as np
 import pytest
 import torch
 
+from kernel_lab import _native
 from kernel_lab.kv_cache import build_paged_kv, device_decode_problem, random_decode_problem
 from oracle import reference as ref
 from tests.conftest import DTYPES, decode_parity
@@ -326,11 +327,11 @@ def test_requested_balanced_schedule_falls_back_for_fp32(gpu_ops):
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize(("hq", "hkv", "head_dim"), [(32, 8, 128), (8, 1, 64), (16, 16, 256)])
-def test_forced_valu_kernel_on_mfma_shapes(gpu_ops, monkeypatch, hq, hkv, head_dim, dtype):
+def test_forced_valu_kernel_on_mfma_shapes(gpu_ops, hq, hkv, head_dim, dtype):
     """KL_DECODE_FORCE_VALU=1 runs the VALU kernel (the benchmarks' comparison
     path) on shapes the MFMA kernel normally takes; both must match the oracle."""
     q, kv, _, _ = random_decode_problem([1, 40, 300, 17], hq, hkv, head_dim, 16, dtype=dtype, device="cuda",
                                         poison=float("nan"))
-    monkeypatch.setenv("KL_DECODE_FORCE_VALU", "1")
-    check(run(gpu_ops, q, kv), expected(q, kv), dtype)
-    check(run(gpu_ops, q, kv, num_splits=3), expected(q, kv), dtype)
+    with _native.decode_switches(force_valu="1"):
+        check(run(gpu_ops, q, kv), expected(q, kv), dtype)
+        check(run(gpu_ops, q, kv, num_splits=3), expected(q, kv), dtype)

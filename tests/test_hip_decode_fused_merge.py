@@ -16,7 +16,6 @@ beyond the library's regions: tests/test_zy_merge_regions.py.
 
 from __future__ import annotations
 
-import os
 
 import pytest
 import torch
@@ -34,15 +33,8 @@ def _decode(ops, q, kv, out=None, **kw):
 
 
 def _unfused(fn):
-    old = os.environ.get("KL_DECODE_FUSED_MERGE")
-    os.environ["KL_DECODE_FUSED_MERGE"] = "0"
-    try:
+    with _native.decode_switches(fused_merge="0"):
         return fn()
-    finally:
-        if old is None:
-            del os.environ["KL_DECODE_FUSED_MERGE"]
-        else:
-            os.environ["KL_DECODE_FUSED_MERGE"] = old
 
 
 def _lens(batch: int, hi: int, seed: int) -> list[int]:

@@ -23,11 +23,10 @@ balanced kernel runs in transposed order).
 
 from __future__ import annotations
 
-import os
-
 import pytest
 import torch
 
+from kernel_lab import _native
 from kernel_lab.kv_cache import device_decode_problem, quantize_fp8, random_decode_problem
 from oracle import reference as ref
 from tests.conftest import decode_parity
@@ -47,15 +46,8 @@ def _empty_rows(batch: int, empty: int) -> list[int]:
 def _both(ops, q, kv, **kw):
     """The decode with pairing as planned and with pairing switched off."""
     paired = ops.paged_decode_attention(q, kv.k_cache, kv.v_cache, kv.block_table, kv.seq_lens, **kw)
-    old = os.environ.get("KL_DECODE_PAIRED")
-    os.environ["KL_DECODE_PAIRED"] = "0"
-    try:
+    with _native.decode_switches(paired="0"):
         single = ops.paged_decode_attention(q, kv.k_cache, kv.v_cache, kv.block_table, kv.seq_lens, **kw)
-    finally:
-        if old is None:
-            del os.environ["KL_DECODE_PAIRED"]
-        else:
-            os.environ["KL_DECODE_PAIRED"] = old
     torch.cuda.synchronize()
     return paired.cpu(), single.cpu()
 
@@ -97,15 +89,8 @@ def test_paired_fp8_cache_matches_unpaired(gpu_ops):
     k8, v8 = kv8.k_cache, kv8.v_cache
     args = (q, k8, v8, kv.block_table, kv.seq_lens)
     paired = gpu_ops.paged_decode_attention(*args, k_scale=ks, v_scale=vs, num_splits=1)
-    old = os.environ.get("KL_DECODE_PAIRED")
-    os.environ["KL_DECODE_PAIRED"] = "0"
-    try:
+    with _native.decode_switches(paired="0"):
         single = gpu_ops.paged_decode_attention(*args, k_scale=ks, v_scale=vs, num_splits=1)
-    finally:
-        if old is None:
-            del os.environ["KL_DECODE_PAIRED"]
-        else:
-            os.environ["KL_DECODE_PAIRED"] = old
     assert torch.equal(paired.cpu(), single.cpu()), "paired workgroups changed the FP8 result"
     want = ref.paged_decode_attention_fp8(
         q.cpu().float(), k8.cpu(), v8.cpu(), kv.block_table.cpu(), kv.seq_lens.cpu(), ks.cpu(), vs.cpu()
