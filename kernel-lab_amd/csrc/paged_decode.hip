@@ -394,12 +394,22 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
   // 4grp + row/4, dims 4(row % 4) .. +3 of each 16-wide tile.
   const S* tr_src = stage + (4 * grp + (row >> 2)) * VROW + 4 * (row & 3);
 
-  // Element offset of this wave's i-th block (wave-uniform, scalar math).
-  auto block_base = [&](int i) -> int64_t {
+  // Element offset of this wave's i-th block in page `page` (wave-uniform,
+  // scalar math).
+  auto page_base = [&](int i, int page) -> int64_t {
     const int blk = first + W * i;
     const int pidx = blk / bpp;
-    return static_cast<int64_t>(bt[pidx]) * a.page_stride +
+    return static_cast<int64_t>(page) * a.page_stride +
            static_cast<int64_t>((blk - pidx * bpp) * kBlock) * a.token_stride + static_cast<int64_t>(u.kvh) * D;
+  };
+  auto block_base = [&](int i) -> int64_t { return page_base(i, bt[(first + W * i) / bpp]); };
+  // The block-table entry of block i by a vector load (every lane reads the
+  // same entry). Inside the main loop the entries come this way, not through
+  // scalar loads: the LDS reads' waits count scalar loads too (one counter),
+  // so a scalar load there made every block wait for the table.
+  const auto btr = make_rsrc(a.block_table + static_cast<int64_t>(u.b) * a.bt_stride);
+  auto page_load = [&](int i) -> float {
+    return buffer_load_f32(btr, static_cast<uint32_t>((first + W * i) / bpp) * 4u);
   };
 
   auto load_block = [&](int64_t base, u32x4 (&kf)[NL], u32x4 (&vf)[NL]) {
@@ -493,21 +503,34 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
     // branch inside, so the compiler's load-wait counts stay exact; slots past
     // the last block re-read the last block (cache-resident) and process it
     // with no valid token, which leaves the running state unchanged.
+    //
+    // Block-table entries run NS blocks ahead of the K/V loads, in a ring of
+    // NS: iteration i turns the entry of block i + NS - 1 (loaded at
+    // iteration i - NS) into the address of that block's K/V loads, then
+    // loads the entry of block i + 2NS - 1 into the freed slot ahead of those
+    // K/V loads. Vector loads complete in order, so the wait for block
+    // i + NS - 1's K/V (in iteration i + NS - 1) also covers that entry before
+    // iteration i + NS uses it: the table costs the loop no wait of its own.
+    // The ring's first entries are loaded before the first blocks' K/V, as
+    // in the loop: the compiler sizes its waits for the worst path into the
+    // loop, and entries loaded after those K/V would make it wait for them on
+    // every iteration.
     u32x4 kb[NS][NL], vb[NS][NL];
-    int64_t next_base = block_base(0);
+    float pg[NS];  // entry bits of blocks i + NS - 1 .. i + 2NS - 2, slot = block % NS
 #pragma unroll
-    for (int s = 0; s < NS - 1; ++s) {
-      load_block(next_base, kb[s], vb[s]);
-      next_base = block_base(min(s + 1, nblk - 1));
-    }
+    for (int k = NS - 1; k < 2 * NS - 1; ++k) pg[k % NS] = page_load(min(k, nblk - 1));
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s) load_block(block_base(min(s, nblk - 1)), kb[s], vb[s]);
     for (int base = 0; base < nblk; base += NS) {
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
         const int i = base + s;
-        const int64_t nb = next_base;
-        load_block(nb, kb[(s + NS - 1) % NS], vb[(s + NS - 1) % NS]);
+        const int slot = (s + NS - 1) % NS;  // block i + NS - 1 (base is a multiple of NS)
+        const int j = min(i + NS - 1, nblk - 1);
+        const int64_t nb = page_base(j, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, pg[slot])));
+        pg[slot] = page_load(min(i + 2 * NS - 1, nblk - 1));
+        load_block(nb, kb[slot], vb[slot]);
         process_block(i, kb[s], vb[s]);
-        next_base = block_base(min(i + NS, nblk - 1));
       }
     }
   }
