@@ -88,6 +88,9 @@ constexpr int kPairMaxSegments = 16;
 constexpr int kBalanceMinPages = 256;
 constexpr size_t kAutoBalanceMaxWorkspace = size_t{16} << 20;
 constexpr float kLog2e = 1.4426950408889634f;
+// How far (log2 units) a score may pass the decode's running reference max
+// before the outputs are rescaled to a new one: weights stay below 2^8.
+constexpr float kRescaleSlack = 8.0f;
 
 struct DecodeArgs {
   const void* q;
@@ -412,9 +415,16 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
     return buffer_load_f32(btr, static_cast<uint32_t>((first + W * i) / bpp) * 4u);
   };
 
-  auto load_block = [&](int64_t base, u32x4 (&kf)[NL], u32x4 (&vf)[NL]) {
-    const auto kr = make_rsrc(kc + base);
-    const auto vr = make_rsrc(vc + base);
+  // A padding slot of the last round (live false) loads through resources of
+  // no records: the hardware answers with zeros and touches no memory, so no
+  // load is still travelling when the waves meet at the merge's barrier
+  // (which waits for every outstanding load).
+  auto load_block = [&](int64_t base, u32x4 (&kf)[NL], u32x4 (&vf)[NL], bool live) {
+    const int records = live ? 0x7fffffff : 0;
+    const auto kr = __builtin_amdgcn_make_buffer_rsrc(const_cast<KS*>(kc + base), static_cast<short>(0), records,
+                                                      kBufferDword3);
+    const auto vr = __builtin_amdgcn_make_buffer_rsrc(const_cast<KS*>(vc + base), static_cast<short>(0), records,
+                                                      kBufferDword3);
 #pragma unroll
     for (int c = 0; c < NL; ++c) kf[c] = buffer_load16<kKvPolicy>(kr, kv_off[c]);
 #pragma unroll
@@ -460,9 +470,14 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
       for (int j = 0; j < 4; ++j) sc[j] = (4 * grp + j < nvalid) ? s[j] * qk_scale : -INFINITY;
       float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
       mx = max_xor32(max_xor16(mx));
-      // A real block's token 0 is valid, so mx is finite; a padding slot has
-      // mx = -inf and comes after at least one real block, so m_new = m.
-      const float m_new = fmaxf(m[t], mx);
+      // The reference max m moves only when a score passes it by more than
+      // kRescaleSlack (log2 units), so the weights p = 2^(s - m) stay below
+      // 2^kRescaleSlack and the outputs are rescaled in few blocks rather
+      // than in most. Any m gives the same softmax: the outputs, the
+      // normaliser and the log-sum-exp all refer to it. A real block's token
+      // 0 is valid, so mx is finite; the first block always moves m off
+      // -inf; a padding slot has mx = -inf and leaves m as it is.
+      const float m_new = mx > m[t] + kRescaleSlack ? mx : m[t];
       grew |= m_new > m[t];
       alpha[t] = __builtin_amdgcn_exp2f(m[t] - m_new);
       float p[4];
@@ -520,7 +535,7 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
 #pragma unroll
     for (int k = NS - 1; k < 2 * NS - 1; ++k) pg[k % NS] = page_load(min(k, nblk - 1));
 #pragma unroll
-    for (int s = 0; s < NS - 1; ++s) load_block(block_base(min(s, nblk - 1)), kb[s], vb[s]);
+    for (int s = 0; s < NS - 1; ++s) load_block(block_base(min(s, nblk - 1)), kb[s], vb[s], s < nblk);
     for (int base = 0; base < nblk; base += NS) {
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
@@ -529,7 +544,7 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
         const int j = min(i + NS - 1, nblk - 1);
         const int64_t nb = page_base(j, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, pg[slot])));
         pg[slot] = page_load(min(i + 2 * NS - 1, nblk - 1));
-        load_block(nb, kb[slot], vb[slot]);
+        load_block(nb, kb[slot], vb[slot], i + NS - 1 < nblk);
         process_block(i, kb[s], vb[s]);
       }
     }
@@ -575,13 +590,16 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
       lw[w] = lds_ml[((w * NT + t) * 16 + row) * 2 + 1];
       mmax = fmaxf(mmax, mw[w]);
     }
+    // Weights 2^(m_w - max) lie in [0, 1]: the hardware exponential suffices
+    // (one whose result is denormal contributes nothing visible).
     float cw[W];
     float denom = 0.0f;
 #pragma unroll
     for (int w = 0; w < W; ++w) {
-      cw[w] = mw[w] == -INFINITY ? 0.0f : exp2f(mw[w] - mmax);
+      cw[w] = mw[w] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw[w] - mmax);
       denom += lw[w] * cw[w];
     }
+    const float inv = out_scale / denom;
     const int hl = h0 + 16 * t + row;
     const bool valid = hl < a.group;
     const int64_t head = q_row(a, u, valid ? hl : 0);
@@ -593,7 +611,7 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
       for (int w = 1; w < W; ++w) num += lds_acc[(w * NT * DT + t * DT + dt) * 64 + lane] * cw[w];
       float o[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = num[i] / denom * out_scale;
+      for (int i = 0; i < 4; ++i) o[i] = num[i] * inv;
       if (!valid) continue;
       const int d = 16 * dt + 4 * grp;
       if (dst.final) {
@@ -611,7 +629,7 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
     if (valid && !dst.final && grp == 0 && (t * DT) % W == wave) {
       buffer_store_f32<kCachePolicyDevice>(make_rsrc(uniform_ptr(dst.lse)),
                                            static_cast<uint32_t>((16 * t + row) * dst.lse_head_stride * 4),
-                                           mmax + log2f(denom));
+                                           mmax + __builtin_amdgcn_logf(denom));
     }
   }
 }
