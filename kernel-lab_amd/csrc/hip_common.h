@@ -274,6 +274,48 @@ __device__ __forceinline__ void wait_vector_memory() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// Waits until at most N of this wave's vector-memory operations are in flight
+// (s_waitcnt vmcnt(N); the other counters unconstrained). They complete in
+// issue order, so every operation issued before the last N is done. The
+// signal fences keep the compiler from moving memory accesses across it.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Non-temporal load straight to LDS (gfx950 buffer_load_dwordx4 ... lds):
+// lane l's 16 bytes at `byte_offset` past `base` land at dst + 16 l; lanes at
+// or past `records` bytes write zeros and read no memory. `base`, `records`
+// and `dst` must be wave-uniform. Issued as an asm statement: the compiler
+// then tracks neither the vmcnt slot it takes nor the LDS it writes, so it
+// adds no waits of its own for it (its tracking of these loads is
+// conservative or absent depending on the address arithmetic), and readers
+// of `dst` must wait explicitly (wait_vmcnt).
+__device__ __forceinline__ void buffer_load16_lds_nt(const void* base, int records, void* dst, uint32_t byte_offset) {
+  typedef int i32x4 __attribute__((ext_vector_type(4)));
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const i32x4 rsrc = {static_cast<int>(static_cast<uint32_t>(b)), static_cast<int>((b >> 32) & 0xffff), records,
+                      kBufferDword3};
+  typedef __attribute__((address_space(3))) char* lds_char;
+  const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_char)(dst)));
+  asm volatile("buffer_load_dwordx4 %1, %2, 0 offen nt lds" ::"{m0}"(lds), "v"(byte_offset), "s"(rsrc) : "memory");
+}
+
+// The 4-byte form of buffer_load16_lds_nt (default cache policy): lane l's
+// dword lands at dst + 4 l.
+__device__ __forceinline__ void buffer_load4_lds(const void* base, int records, void* dst, uint32_t byte_offset) {
+  typedef int i32x4 __attribute__((ext_vector_type(4)));
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const i32x4 rsrc = {static_cast<int>(static_cast<uint32_t>(b)), static_cast<int>((b >> 32) & 0xffff), records,
+                      kBufferDword3};
+  typedef __attribute__((address_space(3))) char* lds_char;
+  const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_char)(dst)));
+  asm volatile("buffer_load_dword %1, %2, 0 offen lds" ::"{m0}"(lds), "v"(byte_offset), "s"(rsrc) : "memory");
+}
+
 // gfx950 transposing LDS read (ds_read_b64_tr_b16). Within each 16-lane row,
 // lane i receives element (i % 4) of the 8-byte chunks addressed by lanes
 // i/4, 4 + i/4, 8 + i/4 and 12 + i/4 of that row, in that order.

@@ -238,24 +238,53 @@ __device__ __forceinline__ uint32_t pack2_residual(float a, float b, uint32_t hi
   return pack2<E>(a - lo_f32<E>(hi), b - hi_f32<E>(hi));
 }
 
+// Depth of the LDS pipeline: blocks per wave in LDS at once. Measured on
+// MI355X (events, same tensors): 3 and 4 stages were slower at every shape
+// tried (32/8/128 fp16 B=8 ctx 4096 30.8 -> 32.9 / 32.3 us, B=1 ctx 4096
+// 16.8 -> 17.6 / 19.3, ragged MQA 45.7 -> 47.7 / 50.2), as deeper register
+// pipelines were: more bytes in flight per wave lower HBM throughput here.
+constexpr int kDmaStages = 2;
+
 // LDS bytes the MFMA kernel needs: the per-wave K and V staging tiles during
 // the main loop, reused for the cross-wave merge afterwards (every wave's
 // output tiles, 16 bytes per lane each, and its running max and normaliser).
-template <int D, int NT, int W = kWaves>
+template <int D, int NT, int W = kWaves, bool DMA = false, int NSD = kDmaStages>
 struct MfmaLds {
-  // Row strides of a staged token. K: 8 elements (16 B) of pad put the 16
-  // rows one ds_read_b128 touches on distinct 16-byte bank groups. V: 16
-  // elements of pad put the 16 rows a transposing read touches on distinct
-  // 32-byte bank groups two by two.
+  // Register pipeline (DMA false): one block per wave staged at a time. Row
+  // strides of a staged token: K's 8 elements (16 B) of pad put the 16 rows
+  // one ds_read_b128 touches on distinct 16-byte bank groups; V's 16 elements
+  // of pad put the 16 rows a transposing read touches on distinct 32-byte
+  // bank groups two by two.
   static constexpr int kKRow = D + 8;
   static constexpr int kVRow = D + 16;
   static constexpr int kWaveStage = kBlock * (kKRow + kVRow);  // elements per wave
-  static constexpr int kStageBytes = W * kWaveStage * 2;
+  // LDS pipeline (DMA true): NSD slots per wave, each one block's K
+  // then V, 16 unpadded rows of D 16-bit elements with their 16-byte chunks
+  // XOR-swizzled by row (the loads place a lane's 16 bytes at a fixed
+  // address, so padding is not available).
+  static constexpr int kDmaSlotBytes = 2 * kBlock * D * 2;
+  // ... followed by a block-table window: two halves of 64 entries.
+  static constexpr int kDmaWaveBytes = NSD * kDmaSlotBytes + 2 * 64 * 4;
+  static constexpr int kStageBytes = DMA ? W * kDmaWaveBytes : W * kWaveStage * 2;
   static constexpr int kAccBytes = W * NT * (D / 16) * 64 * 16;
   static constexpr int kMlBytes = W * NT * 16 * 2 * 4;
   static constexpr int kBytes =
       kStageBytes > kAccBytes + kMlBytes ? kStageBytes : kAccBytes + kMlBytes;
 };
+
+// Whether a segment stages K and V through LDS by direct-to-LDS loads (the
+// LDS pipeline) rather than through registers: 16-bit caches at head_dim 128
+// with one head tile. FP8 codes must be decoded on the way into LDS, so they
+// take registers. Measured on MI355X against the register pipeline (events,
+// same tensors, 3 rounds, 32/8/128 fp16 unless noted): B=32 ctx 512 17.96 ->
+// 17.34 us, B=64 ctx 512 28.12 -> 27.52, B=64 ctx 4096 164.5 -> 163.2, B=1
+// ctx 4096 16.66 -> 16.54, 64/8/128 bf16 B=8 ctx 32768 166.8 -> 165.7, B=8
+// ctx 4096 31.56 -> 31.68; two head tiles (ragged MQA) 44.15 -> 45.91, so
+// those keep registers.
+template <typename KVF, int D, int NT>
+constexpr bool dma_staged() {
+  return !std::is_same_v<KVF, Fp8E4M3> && D == 128 && NT == 1;
+}
 
 // Register pipeline depth: blocks whose K and V are held in VGPRs at once
 // (one being processed, the rest in flight); 8 KiB per block at D = 128 with
@@ -305,7 +334,7 @@ struct Dest {
 // formats share every instruction. An FP8 cache's per-head scales are folded
 // into the score scale (K) and the epilogue (V): q.(s_k k) = s_k (q.k) and
 // sum p (s_v v) = s_v sum p v.
-template <typename E, typename KVF, int D, int NT, int W = kWaves>
+template <typename E, typename KVF, int D, int NT, int W = kWaves, int NSD = kDmaStages>
 __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, const Unit& u, const Dest& dst,
                                              const int wave) {
   using S = typename E::S;
@@ -320,8 +349,10 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
   constexpr int TPL = 64 / LPT;        // tokens per load instruction
   constexpr int NL = kBlock / TPL;     // 16-byte loads per lane per block, each of K and V
   static_assert(TPL <= kBlock && kBlock % TPL == 0, "a load must stay inside its 16-token block");
-  constexpr int KROW = MfmaLds<D, NT, W>::kKRow;
-  constexpr int VROW = MfmaLds<D, NT, W>::kVRow;
+  constexpr bool kDma = dma_staged<KVF, D, NT>();
+  using Lds = MfmaLds<D, NT, W, kDma, NSD>;
+  constexpr int KROW = Lds::kKRow;
+  constexpr int VROW = Lds::kVRow;
   constexpr int NS = mfma_stages<D, NT>();
 
   const int lane = __lane_id();
@@ -390,12 +421,36 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
   // markedly faster than the MFMA operand layout, and are re-laid out through
   // this wave's LDS tiles: K rows are read back as the A operand (lane = token,
   // 8 dims), V through the transposing read.
-  S* kstage = reinterpret_cast<S*>(lds) + wave * MfmaLds<D, NT, W>::kWaveStage;
+  S* kstage = reinterpret_cast<S*>(lds) + wave * Lds::kWaveStage;
   S* stage = kstage + kBlock * KROW;
   const S* k_src = kstage + row * KROW + 8 * grp;
   // Source of this lane's 8-byte chunk in the transposing V^T read: token
   // 4grp + row/4, dims 4(row % 4) .. +3 of each 16-wide tile.
   const S* tr_src = stage + (4 * grp + (row >> 2)) * VROW + 4 * (row & 3);
+
+  // LDS pipeline addressing (kDma). A staged block is 16 rows of D elements;
+  // token t's 16-byte chunk c sits in slot c ^ t of its row, so the 16 rows
+  // one read touches fall on distinct bank groups. Load c puts lane l's 16
+  // bytes at byte c * 1024 + 16 l, i.e. token 4c + l/16, slot l % 16: the
+  // lane reads chunk (l % 16) ^ t of that token, and every 16-lane row still
+  // reads a whole 256-byte token row. Readers XOR a per-lane base with the
+  // chunk's index: the swizzle and the index occupy disjoint address bits.
+  uint32_t dma_off[NL];
+  int k_rd = 0, v_rd = 0;  // element offsets in a slot's K and V rows
+  if constexpr (kDma) {
+    static_assert(D == 128 && NL == 4 && TPL == 4, "the LDS pipeline is laid out for head_dim 128");
+#pragma unroll
+    for (int c = 0; c < NL; ++c) {
+      const int tok = 4 * c + (lane >> 4);
+      const int chunk = (lane & 15) ^ tok;
+      dma_off[c] = static_cast<uint32_t>((tok * a.token_stride + chunk * 8) * 2);
+    }
+    // K as the A operand, chunk c: token `row`, dims 32c + 8grp .. +7.
+    k_rd = row * D + ((grp ^ (row & 3)) << 3) + ((row >> 2) << 5);
+    // V^T: token 4grp + row/4, dims 16dt + 4(row % 4) .. +3.
+    const int tok = 4 * grp + (row >> 2);
+    v_rd = tok * D + ((((row & 3) >> 1) ^ (tok & 1)) << 3) + 4 * (row & 1) + ((tok >> 1) << 4);
+  }
 
   // Element offset of this wave's i-th block in page `page` (wave-uniform,
   // scalar math).
@@ -443,18 +498,14 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
     }
   };
 
-  auto process_block = [&](int i, const u32x4 (&kf)[NL], const u32x4 (&vf)[NL]) {
+  // Scores, online softmax and P V of block i, from its K operand (the A
+  // operand of S = K Q^T: lane holds token `row`, dims 32c + 8grp .. +7),
+  // a stage_v(nvalid) step run before the V tiles are read, and v_tile(dt),
+  // which reads V^T tile dt (lane holds V[token 4grp + j][dim 16dt + row]).
+  auto compute_block = [&](int i, const u32x4 (&ka)[KC], auto&& stage_v, auto&& v_tile) {
     // Valid tokens in the block: >= 16 means all; <= 0 only for the padding
     // slots of the last pipeline round (i >= nblk).
     const int nvalid = i < nblk ? u.seq_len - (first + W * i) * kBlock : 0;
-
-    // Stage K (its rows past seq_len only feed scores replaced by -inf below).
-#pragma unroll
-    for (int c = 0; c < NL; ++c) stage16(kstage + (c * TPL + v_tok) * KROW + v_dim, kf[c]);
-    // K as the A operand of S = K Q^T: lane holds token `row`, dims 32c + 8grp .. +7.
-    u32x4 ka[KC];
-#pragma unroll
-    for (int c = 0; c < KC; ++c) ka[c] = *reinterpret_cast<const u32x4*>(k_src + 32 * c);
 
     // Scores: lane holds S[token 4grp + i][head row] for tile t.
     u32x2 pf[NT], pl[NT];
@@ -497,22 +548,106 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
       }
     }
 
-    // Stage V, rows past seq_len as zeros, for the transposed reads.
-#pragma unroll
-    for (int c = 0; c < NL; ++c) {
-      const int tok = c * TPL + v_tok;
-      stage16(stage + tok * VROW + v_dim, tok < nvalid ? vf[c] : u32x4{0, 0, 0, 0});
-    }
-    // V^T as the A operand: lane holds V[token 4grp + j][dim 16dt + row].
+    stage_v(nvalid);
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      const u32x2 va = lds_read_tr16(tr_src + 16 * dt);
+      const u32x2 va = v_tile(dt);
 #pragma unroll
       for (int t = 0; t < NT; ++t) acc[t][dt] = pv_split<E>(va, pf[t], pl[t], acc[t][dt]);
     }
   };
 
-  if (nblk > 0) {
+  // Register pipeline: block i's K and V arrive in registers (kf, vf) and are
+  // re-laid out through this wave's LDS tile.
+  auto process_block = [&](int i, const u32x4 (&kf)[NL], const u32x4 (&vf)[NL]) {
+    // Stage K (its rows past seq_len only feed scores replaced by -inf).
+#pragma unroll
+    for (int c = 0; c < NL; ++c) stage16(kstage + (c * TPL + v_tok) * KROW + v_dim, kf[c]);
+    u32x4 ka[KC];
+#pragma unroll
+    for (int c = 0; c < KC; ++c) ka[c] = *reinterpret_cast<const u32x4*>(k_src + 32 * c);
+    compute_block(
+        i, ka,
+        [&](int nvalid) {
+          // Stage V, rows past seq_len as zeros, for the transposed reads.
+#pragma unroll
+          for (int c = 0; c < NL; ++c) {
+            const int tok = c * TPL + v_tok;
+            stage16(stage + tok * VROW + v_dim, tok < nvalid ? vf[c] : u32x4{0, 0, 0, 0});
+          }
+        },
+        [&](int dt) { return lds_read_tr16(tr_src + 16 * dt); });
+  };
+
+  // LDS pipeline: block i's K and V load straight into its LDS slot (rows
+  // past seq_len as zeros); K and then V are waited for just before they are
+  // read (the loop's issue order makes both waits exact: see there).
+  auto process_block_lds = [&](int i, const char* slot, auto&& wait_k, auto&& wait_v) {
+    const S* ks = reinterpret_cast<const S*>(slot);
+    const S* vs = ks + kBlock * D;
+    wait_k();
+    u32x4 ka[KC];
+#pragma unroll
+    for (int c = 0; c < KC; ++c) ka[c] = *reinterpret_cast<const u32x4*>(ks + (k_rd ^ (c << 5)));
+    compute_block(i, ka, [&](int) { wait_v(); }, [&](int dt) { return lds_read_tr16(vs + (v_rd ^ (dt << 4))); });
+  };
+
+  if constexpr (kDma) {
+    if (nblk > 0) {
+      // LDS pipeline, NSD deep: while block i is processed from
+      // its slot, blocks i+1 .. i+NSD-1 are loading straight into theirs.
+      // Each iteration issues 8 of these loads (block i + NSD - 1's 4 for K,
+      // then 4 for V; asm statements keep their order), which the compiler
+      // does not see, and they complete in order: once at most
+      // 8 (NSD - 1) + 4 are in flight, block i's K is in LDS, and its V once
+      // at most 8 (NSD - 1) are. (An iteration that also refills the
+      // block-table window issues one more load, first, which only makes
+      // these waits stricter.)
+      //
+      // Block-table entries come the same way, into a window in LDS: half h
+      // holds the entries of blocks 64w .. 64w + 63 for w = h (mod 2), one per
+      // lane of a 4-byte load, and is refilled with w + 2 when the loop
+      // enters window w + 1, 64 blocks before it is read. With no vector load
+      // the compiler can see inside the loop, it adds no waits there.
+      char* slots = lds + wave * Lds::kDmaWaveBytes;
+      int* win = reinterpret_cast<int*>(slots + NSD * Lds::kDmaSlotBytes);
+      const int32_t* bt_row = a.block_table + static_cast<int64_t>(u.b) * a.bt_stride;
+      auto window_load = [&](int w) {
+        const int j = min(64 * w + lane, nblk - 1);
+        buffer_load4_lds(bt_row, a.max_pages * 4, win + (w & 1) * 64,
+                         static_cast<uint32_t>((first + W * j) / bpp) * 4u);
+      };
+      window_load(0);
+      if (nblk > 64) window_load(1);
+      wait_vmcnt<0>();  // the first window is read right away (q's loads land too)
+      auto dma_block = [&](int j, int slot, int valid) {
+        if (j >= 64 && (j & 63) == 0 && 64 * ((j >> 6) + 1) < nblk) window_load((j >> 6) + 1);
+        const int page = __builtin_amdgcn_readfirstlane(win[((j >> 6) & 1) * 64 + (j & 63)]);
+        const int64_t off = page_base(j, page);
+        const int records = valid > 0 ? min(valid, kBlock) * a.token_stride * 2 : 0;
+        char* dst = slots + slot * Lds::kDmaSlotBytes;
+#pragma unroll
+        for (int c = 0; c < NL; ++c) buffer_load16_lds_nt(kc + off, records, dst + c * 1024, dma_off[c]);
+#pragma unroll
+        for (int c = 0; c < NL; ++c) buffer_load16_lds_nt(vc + off, records, dst + kBlock * D * 2 + c * 1024, dma_off[c]);
+      };
+      auto valid_of = [&](int i) { return i < nblk ? u.seq_len - (first + W * i) * kBlock : 0; };
+#pragma unroll
+      for (int k = 0; k < NSD - 1; ++k) dma_block(min(k, nblk - 1), k, valid_of(k));
+      for (int base = 0; base < nblk; base += NSD) {
+#pragma unroll
+        for (int s = 0; s < NSD; ++s) {
+          const int i = base + s;
+          dma_block(min(i + NSD - 1, nblk - 1), (s + NSD - 1) % NSD, valid_of(i + NSD - 1));
+          process_block_lds(i, slots + s * Lds::kDmaSlotBytes, [] { wait_vmcnt<8 * (NSD - 1) + 4>(); },
+                            [] { wait_vmcnt<8 * (NSD - 1)>(); });
+        }
+      }
+      // The last round's loads past the end write zeros into slots that the
+      // cross-wave merge below reuses: let them land first.
+      wait_vmcnt<0>();
+    }
+  } else if (nblk > 0) {
     // NS-stage pipeline: while block i is processed, blocks i+1 .. i+NS-1 are
     // in flight. The loop runs a whole number of NS-block rounds with no
     // branch inside, so the compiler's load-wait counts stay exact; slots past
@@ -812,7 +947,7 @@ __device__ __forceinline__ Dest uniform_dest(const DecodeArgs& a, const Unit& u,
 // split owning pages_per_split pages (the reference's decomposition).
 template <typename E, typename KVF, int D, int NT>
 __global__ void __launch_bounds__(kThreads, (mfma_waves_per_eu<D, NT>())) decode_mfma_kernel(const DecodeArgs a) {
-  __shared__ __attribute__((aligned(16))) char lds[MfmaLds<D, NT>::kBytes];
+  __shared__ __attribute__((aligned(16))) char lds[MfmaLds<D, NT, kWaves, dma_staged<KVF, D, NT>()>::kBytes];
   __shared__ int s_last[1];
   const Unit u = decode_unit(a);
   if (u.page_begin >= u.page_end) {
@@ -843,7 +978,8 @@ __global__ void __launch_bounds__(kThreads, (mfma_waves_per_eu<D, NT>())) decode
 template <typename E, typename KVF, int D, int NT>
 __global__ void __launch_bounds__(2 * kThreads, (mfma_waves_per_eu<D, NT>()))
     decode_mfma_paired_kernel(const DecodeArgs a) {
-  __shared__ __attribute__((aligned(16))) char lds[2 * MfmaLds<D, NT>::kBytes];
+  using Lds = MfmaLds<D, NT, kWaves, dma_staged<KVF, D, NT>()>;
+  __shared__ __attribute__((aligned(16))) char lds[2 * Lds::kBytes];
   __shared__ int s_last[2];
   const int wave = wave_id();
   const int half = wave / kWaves;
@@ -861,7 +997,7 @@ __global__ void __launch_bounds__(2 * kThreads, (mfma_waves_per_eu<D, NT>()))
     return;
   }
   const Dest dst = uniform_dest(a, u, D);
-  mfma_segment<E, KVF, D, NT>(a, lds + half * MfmaLds<D, NT>::kBytes, u, dst, wave - half * kWaves);
+  mfma_segment<E, KVF, D, NT>(a, lds + half * Lds::kBytes, u, dst, wave - half * kWaves);
   if constexpr (NT == 1) {  // see kFusedMergeMaxHeads
     if (!dst.final && a.arrivals != nullptr) {
       arrive_and_merge<E>(unit_counter(a, u), uniform_job<E>(a, u, D, active_splits(a, u)), D, wave - half * kWaves,
@@ -1092,7 +1228,8 @@ template <typename E, typename KVF, int D, int NT, int PAIR>
 __global__ void __launch_bounds__(PAIR * kThreads, (mfma_waves_per_eu<D, NT>()))
     decode_mfma_balanced_kernel(const DecodeArgs a) {
   constexpr int W = kWaves;
-  __shared__ __attribute__((aligned(16))) char lds[PAIR * MfmaLds<D, NT, W>::kBytes];
+  using Lds = MfmaLds<D, NT, W, dma_staged<KVF, D, NT>()>;
+  __shared__ __attribute__((aligned(16))) char lds[PAIR * Lds::kBytes];
   __shared__ int s_last[PAIR];
   // A compile-time 0 with PAIR == 1, so the LDS base stays a constant.
   const int half = PAIR == 2 ? wave_id() / W : 0;
@@ -1178,7 +1315,7 @@ __global__ void __launch_bounds__(PAIR * kThreads, (mfma_waves_per_eu<D, NT>()))
     // The previous segment's waves may still read LDS; before the first
     // segment nothing has used it (the schedule needs no LDS), so no barrier.
     if (pos != st.pos) __syncthreads();
-    mfma_segment<E, KVF, D, NT, W>(a, lds + half * MfmaLds<D, NT, W>::kBytes, u, dst, wave_id() - half * W);
+    mfma_segment<E, KVF, D, NT, W>(a, lds + half * Lds::kBytes, u, dst, wave_id() - half * W);
     if (NT == 1 && !dst.final && a.arrivals != nullptr) {  // see kFusedMergeMaxHeads
       // The unit's segments are workgroups w0 .. w1 (slots (w + list unit) * PAIR + half).
       const int64_t w0 = unit_base / st.per;

@@ -222,6 +222,20 @@ def test_config3_ragged_mqa(gpu_ops):
         check(run(gpu_ops, q, kv, num_splits=splits), want, torch.bfloat16, f"ragged MQA splits={splits}")
 
 
+@pytest.mark.parametrize("page", [16, 32, 64])
+@pytest.mark.parametrize(("dtype", "hq", "splits"), [(torch.float16, 32, 1), (torch.bfloat16, 64, 1), (torch.float16, 32, 2)])
+def test_long_segments_refill_the_block_table_window(gpu_ops, page, dtype, hq, splits):
+    """Head_dim 128 with one head tile loads K and V straight into LDS and
+    reads each wave's block-table entries from a 64-block window in LDS that
+    is refilled ahead of use. Segments of 8,000+ tokens give every wave well
+    over 128 blocks (several refills), the lengths end mid-block and mid-page,
+    and the pages are scattered over the cache."""
+    lens = [8 * 1024 + 5, 6 * 1024 - 1, 9 * 1024 + page + 3]
+    q, kv, _, _ = random_decode_problem(lens, hq, 8, 128, page, dtype=dtype, device="cuda", poison=float("nan"),
+                                        seed=page + hq)
+    check(run(gpu_ops, q, kv, num_splits=splits), expected(q, kv), dtype, f"page {page} splits {splits}")
+
+
 def test_config4_long_context_gqa(gpu_ops):
     """64/8/128/16 bf16, B 8, ctx 32768; the planner picks the splits."""
     q, kv = device_decode_problem([32768] * 8, 64, 8, 128, 16, dtype=torch.bfloat16, seed=4)
