@@ -428,28 +428,32 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
   // 4grp + row/4, dims 4(row % 4) .. +3 of each 16-wide tile.
   const S* tr_src = stage + (4 * grp + (row >> 2)) * VROW + 4 * (row & 3);
 
-  // LDS pipeline addressing (kDma). A staged block is 16 rows of D elements;
-  // token t's 16-byte chunk c sits in slot c ^ t of its row, so the 16 rows
-  // one read touches fall on distinct bank groups. Load c puts lane l's 16
-  // bytes at byte c * 1024 + 16 l, i.e. token 4c + l/16, slot l % 16: the
-  // lane reads chunk (l % 16) ^ t of that token, and every 16-lane row still
-  // reads a whole 256-byte token row. Readers XOR a per-lane base with the
-  // chunk's index: the swizzle and the index occupy disjoint address bits.
-  uint32_t dma_off[NL];
+  // LDS pipeline addressing (kDma). A staged block is 16 rows of D elements
+  // whose 16-byte chunks are permuted within each row: token t's chunk c sits
+  // in slot c ^ t for K and c ^ 2(t % 8) for V, so that the rows one read
+  // phase touches fall on distinct banks (K: 16 rows x 16 bytes; V's
+  // transposing read: 4 rows x 4 pieces of 8 bytes). Load c puts lane l's
+  // 16 bytes at byte c * 1024 + 16 l, i.e. token 4c + l/16, slot l % 16: the
+  // lane reads the chunk that belongs there, and every 16-lane row still
+  // reads one whole 256-byte token row from memory. Readers XOR a per-lane
+  // base with the chunk's index: the permutation and the index occupy
+  // disjoint address bits.
+  uint32_t k_off[NL], v_off[NL];
   int k_rd = 0, v_rd = 0;  // element offsets in a slot's K and V rows
   if constexpr (kDma) {
     static_assert(D == 128 && NL == 4 && TPL == 4, "the LDS pipeline is laid out for head_dim 128");
 #pragma unroll
     for (int c = 0; c < NL; ++c) {
       const int tok = 4 * c + (lane >> 4);
-      const int chunk = (lane & 15) ^ tok;
-      dma_off[c] = static_cast<uint32_t>((tok * a.token_stride + chunk * 8) * 2);
+      const int slot = lane & 15;
+      k_off[c] = static_cast<uint32_t>((tok * a.token_stride + (slot ^ tok) * 8) * 2);
+      v_off[c] = static_cast<uint32_t>((tok * a.token_stride + (slot ^ (2 * (tok & 7))) * 8) * 2);
     }
     // K as the A operand, chunk c: token `row`, dims 32c + 8grp .. +7.
     k_rd = row * D + ((grp ^ (row & 3)) << 3) + ((row >> 2) << 5);
     // V^T: token 4grp + row/4, dims 16dt + 4(row % 4) .. +3.
     const int tok = 4 * grp + (row >> 2);
-    v_rd = tok * D + ((((row & 3) >> 1) ^ (tok & 1)) << 3) + 4 * (row & 1) + ((tok >> 1) << 4);
+    v_rd = tok * D + (((row & 3) >> 1) << 3) + 4 * (row & 1) + ((tok & 7) << 4);
   }
 
   // Element offset of this wave's i-th block in page `page` (wave-uniform,
@@ -627,9 +631,9 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
         const int records = valid > 0 ? min(valid, kBlock) * a.token_stride * 2 : 0;
         char* dst = slots + slot * Lds::kDmaSlotBytes;
 #pragma unroll
-        for (int c = 0; c < NL; ++c) buffer_load16_lds_nt(kc + off, records, dst + c * 1024, dma_off[c]);
+        for (int c = 0; c < NL; ++c) buffer_load16_lds_nt(kc + off, records, dst + c * 1024, k_off[c]);
 #pragma unroll
-        for (int c = 0; c < NL; ++c) buffer_load16_lds_nt(vc + off, records, dst + kBlock * D * 2 + c * 1024, dma_off[c]);
+        for (int c = 0; c < NL; ++c) buffer_load16_lds_nt(vc + off, records, dst + kBlock * D * 2 + c * 1024, v_off[c]);
       };
       auto valid_of = [&](int i) { return i < nblk ? u.seq_len - (first + W * i) * kBlock : 0; };
 #pragma unroll
