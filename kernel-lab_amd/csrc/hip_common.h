@@ -23,6 +23,9 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------- elements
 // Element traits. `S` is the storage type in memory; to_f32/from_f32 are the
@@ -98,10 +101,19 @@ __device__ __forceinline__ float hi_f32(uint32_t w) {
   return E::to_f32(static_cast<uint16_t>(w >> 16));
 }
 
-// Two floats rounded to 16-bit and packed, first in the low half.
+// Two floats rounded to 16-bit and packed, first in the low half. A
+// two-element conversion is one v_cvt_pk_{f16,bf16}_f32 on gfx950 (round to
+// nearest even, as from_f32); converting the halves one by one took two
+// conversions, a shift and an or.
 template <typename E>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
-  return static_cast<uint32_t>(E::from_f32(a)) | (static_cast<uint32_t>(E::from_f32(b)) << 16);
+  if constexpr (std::is_same_v<E, BF16>) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+  } else if constexpr (std::is_same_v<E, F16>) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
+  } else {
+    return static_cast<uint32_t>(E::from_f32(a)) | (static_cast<uint32_t>(E::from_f32(b)) << 16);
+  }
 }
 
 // ------------------------------------------------------------------- DPP

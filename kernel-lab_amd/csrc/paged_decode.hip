@@ -111,6 +111,12 @@ struct DecodeArgs {
   int num_kv_heads;
   int group;            // num_q_heads / num_kv_heads
   int page_size;
+  // Blocks per page (page_size / 16) as a multiplier and shift: for
+  // 0 <= n < 2^31, n / bpp == (n * bpp_magic) >> bpp_shift (set_page_size).
+  // The block -> page division runs for every block of the MFMA loops, where a
+  // division by a run-time integer costs ~20 scalar instructions.
+  uint32_t bpp_magic;
+  int bpp_shift;
   int max_pages;
   int num_splits;
   int pages_per_split;
@@ -131,6 +137,11 @@ struct DecodeArgs {
   // and left zero (null: a merge kernel combines the partials).
   uint32_t* arrivals;
 };
+
+// Block index -> page index (n >= 0, wave-uniform or per lane).
+__device__ __forceinline__ int block_page(const DecodeArgs& a, int n) {
+  return static_cast<int>((static_cast<uint64_t>(static_cast<uint32_t>(n)) * a.bpp_magic) >> a.bpp_shift);
+}
 
 struct Unit {
   int b, kvh, hg, split;
@@ -460,18 +471,18 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
   // scalar math).
   auto page_base = [&](int i, int page) -> int64_t {
     const int blk = first + W * i;
-    const int pidx = blk / bpp;
+    const int pidx = block_page(a, blk);
     return static_cast<int64_t>(page) * a.page_stride +
            static_cast<int64_t>((blk - pidx * bpp) * kBlock) * a.token_stride + static_cast<int64_t>(u.kvh) * D;
   };
-  auto block_base = [&](int i) -> int64_t { return page_base(i, bt[(first + W * i) / bpp]); };
+  auto block_base = [&](int i) -> int64_t { return page_base(i, bt[block_page(a, first + W * i)]); };
   // The block-table entry of block i by a vector load (every lane reads the
   // same entry). Inside the main loop the entries come this way, not through
   // scalar loads: the LDS reads' waits count scalar loads too (one counter),
   // so a scalar load there made every block wait for the table.
   const auto btr = make_rsrc(a.block_table + static_cast<int64_t>(u.b) * a.bt_stride);
   auto page_load = [&](int i) -> float {
-    return buffer_load_f32(btr, static_cast<uint32_t>((first + W * i) / bpp) * 4u);
+    return buffer_load_f32(btr, static_cast<uint32_t>(block_page(a, first + W * i)) * 4u);
   };
 
   // A padding slot of the last round (live false) loads through resources of
@@ -522,7 +533,13 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
       for (int c = 0; c < KC; ++c) s = M::mma(ka[c], qf[t][c], s);
       float sc[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) sc[j] = (4 * grp + j < nvalid) ? s[j] * qk_scale : -INFINITY;
+      for (int j = 0; j < 4; ++j) sc[j] = s[j] * qk_scale;
+      // Only a sequence's last block (and a padding slot) has tokens to mask;
+      // nvalid is wave-uniform, so full blocks skip the selects.
+      if (nvalid < kBlock) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sc[j] = (4 * grp + j < nvalid) ? sc[j] : -INFINITY;
+      }
       float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
       mx = max_xor32(max_xor16(mx));
       // The reference max m moves only when a score passes it by more than
@@ -619,7 +636,7 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
       auto window_load = [&](int w) {
         const int j = min(64 * w + lane, nblk - 1);
         buffer_load4_lds(bt_row, a.max_pages * 4, win + (w & 1) * 64,
-                         static_cast<uint32_t>((first + W * j) / bpp) * 4u);
+                         static_cast<uint32_t>(block_page(a, first + W * j)) * 4u);
       };
       window_load(0);
       if (nblk > 64) window_load(1);
@@ -1837,6 +1854,20 @@ __global__ void __launch_bounds__(64) cascade_merge_kernel(const CascadeArgs c, 
 
 // -------------------------------------------------------------- host side
 
+// Sets the page size and the multiplier / shift of the block -> page
+// division (block_page). With d = blocks per page, l = ceil(log2 d) and
+// p = 31 + l, m = ceil(2^p / d) is below 2^32, and for 0 <= n < 2^31
+// n m / 2^p = n / d + n e / (d 2^p) with e = m d - 2^p in [0, d): the excess
+// is below 2^31 / 2^p = 2^-l <= 1 / d, so the floor is floor(n / d).
+void set_page_size(DecodeArgs& a, int page_size) {
+  a.page_size = page_size;
+  const uint64_t d = static_cast<uint64_t>(std::max(1, page_size / kBlock));
+  int l = 0;
+  while ((uint64_t{1} << l) < d) ++l;
+  a.bpp_shift = 31 + l;
+  a.bpp_magic = static_cast<uint32_t>(((uint64_t{1} << a.bpp_shift) + d - 1) / d);
+}
+
 // Shapes the MFMA kernels serve.
 bool mfma_path(kl_dtype dtype, int head_dim, int page_size) {
   return (dtype == KL_DTYPE_F16 || dtype == KL_DTYPE_BF16) && page_size % kBlock == 0 &&
@@ -2435,7 +2466,7 @@ int decode_entry(kl_dtype dtype, bool kv8, void* out, const void* q, const void*
   a.num_q_heads = num_q_heads;
   a.num_kv_heads = num_kv_heads;
   a.group = num_q_heads / num_kv_heads;
-  a.page_size = page_size;
+  set_page_size(a, page_size);
   a.max_pages = max_pages;
   a.num_splits = p.num_splits;
   a.pages_per_split = p.pages_per_split;
@@ -2750,7 +2781,7 @@ extern "C" int kl_cascade_decode_attention(kl_dtype dtype, void* out, const void
   a.num_q_heads = num_q_heads;
   a.num_kv_heads = num_kv_heads;
   a.group = num_q_heads / num_kv_heads;
-  a.page_size = page_size;
+  set_page_size(a, page_size);
   a.grid = 0;
   a.paired = 0;
   a.arrivals = nullptr;

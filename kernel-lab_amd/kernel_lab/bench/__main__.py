@@ -146,6 +146,7 @@ def measure(
         rows.append(Row(kernel, shape, name, round(us, 2), round(gbps, 1),
                         None if share is None else round(100 * share, 1),
                         round(base_us / us, 2) if base_us else None, err, flag))
+    print(f"measured {kernel} {shape}: {len(elapsed)} of {len(impls)} timed", file=sys.stderr, flush=True)
     return rows
 
 
