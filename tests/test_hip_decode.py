@@ -95,6 +95,20 @@ def test_other_page_sizes(gpu_ops, page_size):
     check(run(gpu_ops, q, kv), expected(q, kv), torch.float16)
 
 
+@pytest.mark.parametrize("page_size", [48, 80, 112])
+@pytest.mark.parametrize(("hq", "hkv", "head_dim", "splits"), [(32, 8, 128, 0), (32, 1, 128, 0), (8, 2, 64, 3), (16, 4, 128, -1)])
+def test_page_sizes_not_powers_of_two(gpu_ops, page_size, hq, hkv, head_dim, splits):
+    """Page sizes that are multiples of 16 but not powers of two: the MFMA
+    kernels turn a 16-token block index into its page with a multiply and a
+    shift (3, 5 or 7 blocks per page here). Lengths end mid-block, mid-page
+    and on page boundaries, and the longest gives every wave blocks across
+    many pages."""
+    lens = [1, 15, 16, page_size - 1, page_size, page_size + 17, 40 * page_size + 3]
+    q, kv, _, _ = random_decode_problem(lens, hq, hkv, head_dim, page_size, dtype=torch.bfloat16, device="cuda",
+                                        poison=float("nan"), seed=page_size + hq)
+    check(run(gpu_ops, q, kv, num_splits=splits), expected(q, kv), torch.bfloat16, f"page {page_size} splits {splits}")
+
+
 @pytest.mark.parametrize("poison", [1e4, float("nan")])
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_reads_only_pages_in_the_block_table(gpu_ops, poison, dtype):
