@@ -160,7 +160,9 @@ __device__ __forceinline__ void unit_pages(const DecodeArgs& a, Unit& u) {
   u.page_end = min(u.page_begin + a.pages_per_split, num_pages);
 }
 
-__device__ __forceinline__ Unit decode_unit(const DecodeArgs& a) {
+// The unit of a uniform-split workgroup: b, kvh, hg and split from the
+// workgroup index (no memory access), then its length and page range.
+__device__ __forceinline__ Unit decode_unit_ids(const DecodeArgs& a) {
   Unit u;
   int idx = static_cast<int>(blockIdx.x);
   u.split = idx % a.num_splits;
@@ -169,6 +171,11 @@ __device__ __forceinline__ Unit decode_unit(const DecodeArgs& a) {
   idx /= a.head_groups;
   u.kvh = idx % a.num_kv_heads;
   u.b = idx / a.num_kv_heads;
+  return u;
+}
+
+__device__ __forceinline__ Unit decode_unit(const DecodeArgs& a) {
+  Unit u = decode_unit_ids(a);
   unit_pages(a, u);
   return u;
 }
@@ -177,7 +184,7 @@ __device__ __forceinline__ Unit decode_unit(const DecodeArgs& a) {
 // heads 2j and 2j+1 of one (sequence, head group, split), half `half`
 // taking KV head 2j + half. The digits of i are split (fastest), head
 // group, KV-head pair j, sequence.
-__device__ __forceinline__ Unit decode_unit_paired(const DecodeArgs& a, int half) {
+__device__ __forceinline__ Unit decode_unit_paired_ids(const DecodeArgs& a, int half) {
   Unit u;
   int idx = static_cast<int>(blockIdx.x);
   u.split = idx % a.num_splits;
@@ -187,7 +194,6 @@ __device__ __forceinline__ Unit decode_unit_paired(const DecodeArgs& a, int half
   const int pairs = a.num_kv_heads / 2;
   u.kvh = 2 * (idx % pairs) + half;
   u.b = idx / pairs;
-  unit_pages(a, u);
   return u;
 }
 
@@ -334,6 +340,87 @@ struct Dest {
   int lse_head_stride;
 };
 
+// Makes the kernel fetch its launch arguments together at entry. The
+// compiler loads a kernel argument where it is first needed and waits for each
+// such load in turn; the uniform decode kernel's prologue showed three
+// dependent argument round trips before its first q load. Naming the fields
+// the kernels read as inputs of an empty asm statement has them loaded before
+// it, with one wait.
+__device__ __forceinline__ void fetch_args(const DecodeArgs& a) {
+  asm volatile("" ::"s"(a.q), "s"(a.k), "s"(a.v), "s"(a.out), "s"(a.block_table), "s"(a.seq_lens), "s"(a.o_part),
+               "s"(a.lse_part), "s"(a.bt_stride), "s"(a.page_stride), "s"(a.arrivals));
+  asm volatile("" ::"s"(a.token_stride), "s"(a.batch), "s"(a.num_q_heads), "s"(a.num_kv_heads), "s"(a.group),
+               "s"(a.page_size), "s"(a.bpp_magic), "s"(a.bpp_shift), "s"(a.max_pages), "s"(a.num_splits),
+               "s"(a.pages_per_split), "s"(a.head_groups), "s"(a.heads_per_wg), "s"(a.grid), "s"(a.scale_log2),
+               "s"(a.q_fold), "s"(a.q_heads), "s"(a.force_partial));
+}
+
+// Q as the B operand of S = K Q^T for unit (b, kvh, hg): lane holds head
+// h0 + 16t + row, dims 32c + 8grp .. +7 of chunk c (a lane whose head is past
+// the group reads the group's first head; mfma_segment zeroes it). It depends
+// on the unit alone, not on seq_lens, so a kernel can issue these loads before
+// it waits for the sequence length. Nothing here uses the loaded values: the
+// compiler's wait for them lands where mfma_segment first does, before its
+// main loop.
+template <int NT, int KC>
+struct QFrag {
+  u32x4 v[NT][KC];
+};
+
+template <typename E, int D, int NT>
+__device__ __forceinline__ void load_q(const DecodeArgs& a, const Unit& u, QFrag<NT, D / 32>& qf) {
+  using S = typename E::S;
+  const int lane = __lane_id();
+  const int row = lane & 15;
+  const int grp = lane >> 4;
+  const int h0 = u.hg * a.heads_per_wg;
+  const S* q = static_cast<const S*>(a.q);
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int hl = h0 + 16 * t + row;
+    const S* qh = q + q_row(a, u, hl < a.group ? hl : 0) * D;
+#pragma unroll
+    for (int c = 0; c < D / 32; ++c) qf.v[t][c] = *reinterpret_cast<const u32x4*>(qh + 32 * c + 8 * grp);
+  }
+}
+
+// Block-table window of one wave of the LDS pipeline (see mfma_segment): half
+// h holds the entries of the wave's blocks first + W (64 w + lane) for window
+// w = h (mod 2), the lane's block clamped to the wave's last block (nblk of
+// them). One 4-byte load per lane straight into LDS.
+template <int W>
+__device__ __forceinline__ void dma_window_load(const DecodeArgs& a, int* win, int b, int first, int nblk, int w) {
+  const int j = min(64 * w + __lane_id(), nblk - 1);
+  buffer_load4_lds(a.block_table + static_cast<int64_t>(b) * a.bt_stride, a.max_pages * 4, win + (w & 1) * 64,
+                   static_cast<uint32_t>(block_page(a, first + W * j)) * 4u);
+}
+
+template <int D, int NT, int W, int NSD>
+__device__ __forceinline__ int* dma_window(char* lds, int wave) {
+  using Lds = MfmaLds<D, NT, W, true, NSD>;
+  return reinterpret_cast<int*>(lds + wave * Lds::kDmaWaveBytes + NSD * Lds::kDmaSlotBytes);
+}
+
+// Issues, before seq_lens is known, the first two window halves of this
+// wave's part of a segment of sequence b that starts at page page_begin, as
+// if the sequence reached page page_cap. mfma_segment with win_ready skips
+// its own first window loads: the entries it reads (the sequence's blocks)
+// are the same, and entries past its last block are never read. A caller
+// that returns without running the segment must wait for these loads first.
+template <typename KVF, int D, int NT, int W = kWaves, int NSD = kDmaStages>
+__device__ __forceinline__ void prefetch_window(const DecodeArgs& a, char* lds, int b, int page_begin, int page_cap,
+                                                int wave) {
+  if constexpr (dma_staged<KVF, D, NT>()) {
+    const int bpp = a.page_size / kBlock;
+    const int first = page_begin * bpp + wave;
+    const int blk_cap = page_cap * bpp;
+    const int ncap = first < blk_cap ? (blk_cap - first + W - 1) / W : 0;
+    int* win = dma_window<D, NT, W, NSD>(lds, wave);
+    if (ncap > 0) dma_window_load<W>(a, win, b, first, ncap, 0);
+    if (ncap > 64) dma_window_load<W>(a, win, b, first, ncap, 1);
+  }
+}
+
 // One unit segment on the MFMA path: pages [u.page_begin, u.page_end) of
 // KV head u.kvh, head group u.hg of sequence u.b, by all waves of the
 // workgroup. Contains two workgroup barriers, reached by every wave; on
@@ -345,9 +432,14 @@ struct Dest {
 // formats share every instruction. An FP8 cache's per-head scales are folded
 // into the score scale (K) and the epilogue (V): q.(s_k k) = s_k (q.k) and
 // sum p (s_v v) = s_v sum p v.
+//
+// qpre: the unit's Q fragments, already loaded by the caller (load_q), or
+// null. win_ready: the caller has issued this wave's first block-table window
+// loads for this segment (prefetch_window); LDS pipeline only.
 template <typename E, typename KVF, int D, int NT, int W = kWaves, int NSD = kDmaStages>
 __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, const Unit& u, const Dest& dst,
-                                             const int wave) {
+                                             const int wave, const QFrag<NT, D / 32>* qpre = nullptr,
+                                             const bool win_ready = false) {
   using S = typename E::S;
   using KS = typename KVF::S;          // cache storage type
   using M = Mfma<E>;
@@ -371,21 +463,20 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
   const int grp = lane >> 4;  // MFMA k-group of this lane
   const int h0 = u.hg * a.heads_per_wg;
 
-  // Q as the B operand of S = K Q^T: lane holds head (h0 + 16t + row), dims
-  // 32c + 8grp .. +7 for chunk c. Heads past the group are zero.
+  // Q as the B operand of S = K Q^T (load_q); heads past the group are zero.
   u32x4 qf[NT][KC];
   {
-    const S* q = static_cast<const S*>(a.q);
+    QFrag<NT, KC> raw;
+    if (qpre != nullptr) {
+      raw = *qpre;
+    } else {
+      load_q<E, D, NT>(a, u, raw);
+    }
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const int hl = h0 + 16 * t + row;
-      const bool valid = hl < a.group;
-      const S* qh = q + q_row(a, u, valid ? hl : 0) * D;
+      const bool valid = h0 + 16 * t + row < a.group;
 #pragma unroll
-      for (int c = 0; c < KC; ++c) {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(qh + 32 * c + 8 * grp);
-        qf[t][c] = valid ? v : u32x4{0, 0, 0, 0};
-      }
+      for (int c = 0; c < KC; ++c) qf[t][c] = valid ? raw.v[t][c] : u32x4{0, 0, 0, 0};
     }
   }
 
@@ -631,15 +722,12 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
       // enters window w + 1, 64 blocks before it is read. With no vector load
       // the compiler can see inside the loop, it adds no waits there.
       char* slots = lds + wave * Lds::kDmaWaveBytes;
-      int* win = reinterpret_cast<int*>(slots + NSD * Lds::kDmaSlotBytes);
-      const int32_t* bt_row = a.block_table + static_cast<int64_t>(u.b) * a.bt_stride;
-      auto window_load = [&](int w) {
-        const int j = min(64 * w + lane, nblk - 1);
-        buffer_load4_lds(bt_row, a.max_pages * 4, win + (w & 1) * 64,
-                         static_cast<uint32_t>(block_page(a, first + W * j)) * 4u);
-      };
-      window_load(0);
-      if (nblk > 64) window_load(1);
+      int* win = dma_window<D, NT, W, NSD>(lds, wave);
+      auto window_load = [&](int w) { dma_window_load<W>(a, win, u.b, first, nblk, w); };
+      if (!win_ready) {
+        window_load(0);
+        if (nblk > 64) window_load(1);
+      }
       wait_vmcnt<0>();  // the first window is read right away (q's loads land too)
       auto dma_block = [&](int j, int slot, int valid) {
         if (j >= 64 && (j & 63) == 0 && 64 * ((j >> 6) + 1) < nblk) window_load((j >> 6) + 1);
@@ -666,6 +754,10 @@ __device__ __forceinline__ void mfma_segment(const DecodeArgs& a, char* lds, con
       }
       // The last round's loads past the end write zeros into slots that the
       // cross-wave merge below reuses: let them land first.
+      wait_vmcnt<0>();
+    } else if (win_ready) {
+      // A wave with no block of this segment still has the caller's window
+      // loads in flight into LDS that the cross-wave merge reuses.
       wait_vmcnt<0>();
     }
   } else if (nblk > 0) {
@@ -970,15 +1062,26 @@ template <typename E, typename KVF, int D, int NT>
 __global__ void __launch_bounds__(kThreads, (mfma_waves_per_eu<D, NT>())) decode_mfma_kernel(const DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[MfmaLds<D, NT, kWaves, dma_staged<KVF, D, NT>()>::kBytes];
   __shared__ int s_last[1];
-  const Unit u = decode_unit(a);
+  fetch_args(a);
+  // q and the first block-table window depend on the unit alone: they are
+  // issued before the kernel waits for seq_lens, so the first K/V loads
+  // follow one memory round trip after it instead of two.
+  Unit u = decode_unit_ids(a);
+  const int wave = wave_id();
+  QFrag<NT, D / 32> q;
+  load_q<E, D, NT>(a, u, q);
+  const int pb = u.split * a.pages_per_split;
+  prefetch_window<KVF, D, NT>(a, lds, u.b, pb, min(pb + a.pages_per_split, a.max_pages), wave);
+  unit_pages(a, u);
   if (u.page_begin >= u.page_end) {
+    wait_vmcnt<0>();  // the window loads write this workgroup's LDS
     if (u.split == 0 && u.seq_len <= 0 && (a.num_splits == 1 || a.arrivals != nullptr) && !a.force_partial) {
       write_zero_heads<typename E::S, E>(a, u, D, threadIdx.x, blockDim.x);
     }
     return;  // a split past the end of its sequence has no work
   }
   const Dest dst = uniform_dest(a, u, D);
-  mfma_segment<E, KVF, D, NT>(a, lds, u, dst, wave_id());
+  mfma_segment<E, KVF, D, NT>(a, lds, u, dst, wave, &q, true);
   if constexpr (NT == 1) {  // see kFusedMergeMaxHeads
     if (!dst.final && a.arrivals != nullptr) {
       arrive_and_merge<E>(unit_counter(a, u), uniform_job<E>(a, u, D, active_splits(a, u)), D, wave_id(), s_last);
@@ -1007,8 +1110,17 @@ __global__ void __launch_bounds__(2 * kThreads, (mfma_waves_per_eu<D, NT>()))
   // Both halves hold the same sequence and split, so they agree on whether
   // there is work, whether it is final and how many segments the unit has:
   // they pass the same workgroup barriers.
-  const Unit u = decode_unit_paired(a, half);
+  fetch_args(a);
+  // q and the first block-table window before seq_lens (decode_mfma_kernel).
+  Unit u = decode_unit_paired_ids(a, half);
+  QFrag<NT, D / 32> q;
+  load_q<E, D, NT>(a, u, q);
+  const int pb = u.split * a.pages_per_split;
+  prefetch_window<KVF, D, NT>(a, lds + half * Lds::kBytes, u.b, pb, min(pb + a.pages_per_split, a.max_pages),
+                              wave - half * kWaves);
+  unit_pages(a, u);
   if (u.page_begin >= u.page_end) {
+    wait_vmcnt<0>();  // the window loads write this workgroup's LDS
     // The other half's segment passes two workgroup barriers: pass them too.
     __syncthreads();
     __syncthreads();
@@ -1018,7 +1130,7 @@ __global__ void __launch_bounds__(2 * kThreads, (mfma_waves_per_eu<D, NT>()))
     return;
   }
   const Dest dst = uniform_dest(a, u, D);
-  mfma_segment<E, KVF, D, NT>(a, lds + half * Lds::kBytes, u, dst, wave - half * kWaves);
+  mfma_segment<E, KVF, D, NT>(a, lds + half * Lds::kBytes, u, dst, wave - half * kWaves, &q, true);
   if constexpr (NT == 1) {  // see kFusedMergeMaxHeads
     if (!dst.final && a.arrivals != nullptr) {
       arrive_and_merge<E>(unit_counter(a, u), uniform_job<E>(a, u, D, active_splits(a, u)), D, wave - half * kWaves,
@@ -1252,29 +1364,12 @@ __global__ void __launch_bounds__(PAIR * kThreads, (mfma_waves_per_eu<D, NT>()))
   using Lds = MfmaLds<D, NT, W, dma_staged<KVF, D, NT>()>;
   __shared__ __attribute__((aligned(16))) char lds[PAIR * Lds::kBytes];
   __shared__ int s_last[PAIR];
+  fetch_args(a);
   // A compile-time 0 with PAIR == 1, so the LDS base stays a constant.
   const int half = PAIR == 2 ? wave_id() / W : 0;
   const int hp = a.num_kv_heads * a.head_groups / PAIR;  // list units per sequence
   const int w = PAIR == 2 ? paired_list_wg(a, hp) : static_cast<int>(blockIdx.x);
-  // Where this workgroup would start if every sequence had max_pages pages:
-  // its block-table entry is fetched now, alongside the seq_lens loads the
-  // schedule waits for. On such a batch the guess is exact and the segment's
-  // own load of the entry finds it cached, instead of making a second
-  // dependent trip to memory after the schedule (the uniform-split kernel
-  // needs no guess: its first page is known before it reads seq_lens). A wrong
-  // guess costs one load inside the block table.
-  int32_t guessed_page = 0;
-  {
-    const int64_t seq_span = static_cast<int64_t>(hp) * a.max_pages;
-    const int64_t full = static_cast<int64_t>(a.batch) * seq_span;
-    const int64_t pos = static_cast<int64_t>(w) * balanced_per(a, full);
-    if (pos < full) {
-      const int gb = static_cast<int>(pos / seq_span);
-      guessed_page = as_constant(a.block_table + static_cast<int64_t>(gb) * a.bt_stride)[pos % a.max_pages];
-    }
-  }
   const Start st = schedule_start(a, hp, w);
-  asm volatile("; block-table entry prefetched: %0" ::"s"(guessed_page));
   if (a.arrivals != nullptr) {
     // No merge kernel follows: empty sequences get their zeros here, sequence
     // b from workgroup b % grid (up to 64 * kScanChunks from the schedule's scan).
