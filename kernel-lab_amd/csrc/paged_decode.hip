@@ -68,6 +68,7 @@ constexpr int kThreads = kWaves * 64;
 constexpr int kBlock = 16;     // tokens per MFMA block
 constexpr int kMaxPlannedSplits = 64;
 constexpr int kMinPagesPerSplit = 16;      // fewest pages a planned uniform split takes
+constexpr int kMinPagesPerSingleSplit = 8;  // the same for a batch of one sequence
 constexpr int kMinPagesPerBalancedWg = 8;  // fewest pages a balanced-schedule workgroup takes
 // Cache policy of the K/V loads: streamed once, so non-temporal. Measured on
 // 32/8/128 fp16 B=64 ctx 4096: nt 173 us, nt with sc0 and/or sc1 172.5-173.7,
@@ -916,13 +917,16 @@ constexpr int kArrivalCounters = 8192;   // units per region (8 MiB per device i
 constexpr int kFusedMergeMaxHeads = 8;
 // The last arriver's four waves merge the unit serially: each takes
 // cdiv(heads, 4) heads of `segments` partials, where the merge kernel gives
-// every (sequence, head) its own wave. Measured on MI355X (events, fused vs
-// merge kernel), by heads per wave x segments: 16-32 faster (32/8/128 B=1
-// ctx 4096 16.8 vs 18.2 us, ctx 32768 35.3 vs 37.3), 64 even (37.5 vs 36.4),
-// 128-512 slower (8/1/128 B=1 ctx 8192 22.6 vs 18.1, 32/4/128 B=1 ctx 32768
-// 31.9 vs 28.0, 8/1/128 B=1 ctx 32768 54.5 vs 28.7): few units split over
-// the whole device keep the merge kernel.
-constexpr int kFusedMergeMaxWork = 32;
+// every (sequence, head) its own wave. Measured on MI355X (events, us, same
+// uniform splits, fused vs merge kernel), by heads per wave x segments: 8-16
+// mostly faster (64/8/128 B=1 ctx 4096 S=8 15.1 vs 15.8, 8/1/128 B=8 ctx
+// 4096 S=8 14.3 vs 15.0, 32/8/128 B=1 ctx 8192 S=16 16.2 vs 16.7; with 16
+// short segments slower: 32/8/128 B=2 ctx 2048 S=16 14.1 vs 12.8), 32
+// slower (32/8/128 B=1 ctx 4096 S=32 15.2 vs 13.2, B=2 S=32 20.9 vs 15.8,
+// 64/8/128 B=1 S=16 14.8 vs 13.6), 64-512 slower still (8/1/128 B=1 ctx
+// 8192 22.6 vs 18.1, 32/4/128 B=1 ctx 32768 31.9 vs 28.0): few units split
+// over the whole device keep the merge kernel.
+constexpr int kFusedMergeMaxWork = 16;
 
 __device__ uint32_t g_decode_arrivals[kArrivalRegions * kArrivalCounters];
 
@@ -2232,8 +2236,16 @@ int make_plan(const Options& opt, kl_dtype dtype, int batch, int num_q_heads, in
   // ctx 2048 169.0 vs 174.2) while the worst skew costs less.
   const int full_batch_choice = opt.balance();  // 1 balanced, 0 uniform, -1 by table length
   const bool requested = num_splits == KL_SPLITS_BALANCED;
+  // One sequence cannot be skewed: uniform splits cut it as evenly as the
+  // balanced schedule would, without its start (the seq_lens scan before the
+  // first block-table load) or its merge's search for each unit's slots.
+  // Measured on MI355X (events, us, balanced -> uniform, 32/8/128 fp16 B=1):
+  // ctx 512 11.24 -> 9.92, ctx 4096 16.28 -> 13.20, ctx 32768 33.04 -> 31.76;
+  // 8/1/128 ctx 32768 26.08 -> 16.40.
+  const bool single = batch == 1 && !long_pairs;
   const bool automatic =
-      num_splits == 0 && (units < cus || (full_batch_choice < 0 ? pages >= kBalanceMinPages : full_batch_choice == 1));
+      num_splits == 0 && !single &&
+      (units < cus || (full_batch_choice < 0 ? pages >= kBalanceMinPages : full_batch_choice == 1));
   const bool balance = requested || automatic;
   const bool pair_balanced = pairable && balance;
   if (mfma && !partials && balance) {
@@ -2244,8 +2256,11 @@ int make_plan(const Options& opt, kl_dtype dtype, int batch, int num_q_heads, in
     // workgroups would run in rounds, each paying the schedule's start.
     const int64_t floor_wgs =
         pair_balanced ? static_cast<int64_t>(cus) : std::max<int64_t>(cus, lunits);
-    const int64_t grid =
-        std::max<int64_t>(1, std::min<int64_t>({cdiv(upper, kMinPagesPerBalancedWg), floor_wgs, 0x7fffffffLL}));
+    // At most kMaxPlannedSplits workgroups per list unit, as for uniform
+    // splits: 8/1/128 fp16 B=2 ctx 32768 took 22.1 us as 256 workgroups (128
+    // per sequence) and 17.2 us as 64 uniform splits.
+    const int64_t grid = std::max<int64_t>(
+        1, std::min<int64_t>({cdiv(upper, kMinPagesPerBalancedWg), floor_wgs, lunits * kMaxPlannedSplits, 0x7fffffffLL}));
     p->grid = static_cast<int>(grid);
     p->paired = pair_balanced;
     p->num_splits = 0;
@@ -2267,9 +2282,12 @@ int make_plan(const Options& opt, kl_dtype dtype, int batch, int num_q_heads, in
     // choose_num_splits, kernel_lab/triton_kernels/paged_attention.py:169-173,
     // retuned on MI355X: one 4-wave workgroup per CU beat two for every split
     // count measured, and splits under 16 pages lose more to the merge than
-    // they gain in parallelism).
+    // they gain in parallelism). A single sequence takes splits of 8 pages:
+    // 32/8/128 fp16 B=1 (events, us) ctx 512 S=4 9.9 vs S=2 10.9, ctx 1024
+    // S=8 10.0 vs S=4 11.2, ctx 4096 S=32 13.2 vs S=16 13.4-13.5.
     const int64_t wanted = cdiv(cus, units);
-    const int64_t cap = std::max<int64_t>(1, std::min<int64_t>(cdiv(pages, kMinPagesPerSplit), kMaxPlannedSplits));
+    const int min_pages = batch == 1 && !partials ? kMinPagesPerSingleSplit : kMinPagesPerSplit;
+    const int64_t cap = std::max<int64_t>(1, std::min<int64_t>(cdiv(pages, min_pages), kMaxPlannedSplits));
     s = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(wanted, cap)));
   }
   // Normalise: drop splits no sequence can reach (paged_attention.py:210-211).

@@ -75,7 +75,9 @@ def test_decode_argument_errors_need_no_gpu():
     [
         (64, 8, 256, 256, 1),  # 512 units already fill 256 CUs
         (32, 8, 256, 256, 1),  # 256 units: one per CU
-        (1, 8, 256, 256, 16),  # 32 would be wanted; splits keep >= 16 pages
+        (1, 8, 256, 256, 32),  # one sequence: splits keep >= 8 pages
+        (1, 8, 64, 256, 8),
+        (2, 8, 256, 256, 16),  # several sequences: splits keep >= 16 pages
         (8, 8, 256, 256, 4),
         (8, 8, 2048, 256, 4),
         (1, 1, 3, 256, 1),  # a 3-page table is one split
@@ -102,8 +104,10 @@ def test_planner_fills_the_device(batch, hkv, max_pages, cus, want):
         (32, 8, 4096, True),
         (1024, 16, 8192, False),  # balanced workspace would exceed 16 MiB: uniform
         (8, 8, 256, True),  # fewer units than CUs: balanced at any table length
-        (1, 8, 32, True),
+        (2, 8, 32, True),
         (64, 1, 512, True),
+        (1, 8, 32, False),  # one sequence cannot be skewed: uniform splits
+        (1, 1, 2048, False),
     ],
 )
 def test_planner_balances_uneven_batches_by_default(batch, hkv, max_pages, balanced):
@@ -115,6 +119,9 @@ def test_planner_balances_uneven_batches_by_default(batch, hkv, max_pages, balan
     splits, ws = ops.plan_decode(torch.float16, batch, hkv * 4, hkv, 128, 16, max_pages, 0, 256)
     if balanced:
         assert splits == 0 and 0 < ws <= 16 << 20
+    elif batch == 1:
+        # The uniform rule with >= 8 pages per split, at most 64 splits.
+        assert splits == min(-(-256 // hkv), -(-max_pages // 8), 64) and ws > 0
     else:
         assert splits == 1 and ws == 0
 
@@ -152,20 +159,22 @@ def _align(n: int) -> int:
         (8, 8, 1024, True),  # exactly 128 pages per half
         (8, 8, 1023, False),
         (8, 8, 256, False),  # 32 pages per half: the 8-wave start costs more than pairing gains
-        (1, 8, 8192, False),  # 4 pair units: 64 segments each
+        (2, 8, 8192, False),  # 8 pair units: 32 segments each
         (12, 2, 8192, False),  # 12 pair units: more than 16 segments each
         (8, 1, 32768, False),  # one KV head: nothing to pair
+        (2, 1, 2048, False),  # at most 64 workgroups per list unit
     ],
 )
 def test_planner_pairs_long_contexts_of_small_batches(batch, hkv, max_pages, paired):
     """Fewer units than CUs (balanced by default): the list runs in KV-head
     pairs when every workgroup half gets >= 128 pages and a pair unit at most
     16 segments. The workspace is exact: a partial slot per list workgroup and
-    list unit, two per slot when paired."""
+    list unit, two per slot when paired; a list unit takes at most 64
+    workgroups."""
     splits, ws = ops.plan_decode(torch.float16, batch, hkv * 4, hkv, 128, 16, max_pages, 0, 256)
     units = batch * hkv
     lunits = units // 2 if paired else units
-    grid = min(256, -(-lunits * max_pages // 8))
+    grid = min(256, -(-lunits * max_pages // 8), lunits * 64)
     slots = (grid + lunits) * (2 if paired else 1)
     assert splits == 0
     assert ws == _align(slots * 4 * 128 * 4) + _align(slots * 4 * 4)

@@ -30,6 +30,8 @@ int main(void) {
   printf("plan64long %d %d %d\n", st, splits, ws > 0);
   st = kl_paged_decode_plan(KL_DTYPE_F16, 1, 32, 8, 128, 16, 256, 0, 256, &splits, &ws);
   printf("plan1 %d %d %d\n", st, splits, ws > 0);
+  st = kl_paged_decode_plan(KL_DTYPE_F16, 4, 32, 8, 128, 16, 256, 0, 256, &splits, &ws);
+  printf("plan4 %d %d %d\n", st, splits, ws > 0);
   st = kl_paged_decode_plan(KL_DTYPE_F16, 64, 32, 8, 128, 16, 256, KL_SPLITS_BALANCED, 256, &splits, &ws);
   printf("planbal %d %d %d\n", st, splits, ws > 0);
   size_t cws = 0;
@@ -67,7 +69,8 @@ def test_header_compiles_as_c99_and_links(tmp_path):
     st, splits, ws = got["plan64"].split()
     assert st == "0" and splits == "1" and int(ws) == 0  # one uniform split fills the device
     assert got["plan64long"] == "0 0 1"  # a long table on a full batch: balanced
-    assert got["plan1"] == "0 0 1"  # balanced schedule for a batch of one
+    assert got["plan1"] == "0 32 1"  # one sequence: 32 uniform splits of 8 pages
+    assert got["plan4"] == "0 0 1"  # a few sequences: balanced schedule
     assert got["planbal"] == "0 0 1"
     assert got["cascade"] == "0 1"
     assert got["badgroup"].startswith("1 ") and "multiple" in got["badgroup"]

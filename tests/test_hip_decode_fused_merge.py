@@ -51,7 +51,8 @@ def _last_merge() -> int:
 
 CASES = [
     # (lens, hq, hkv, head_dim, dtype, num_splits, empty rows, merge); None = planner
-    ([512], 32, 8, 128, torch.float16, None, [], IN_KERNEL),  # balanced, B=1
+    ([512], 32, 8, 128, torch.float16, None, [], IN_KERNEL),  # B=1: uniform splits
+    ([512, 500], 32, 8, 128, torch.float16, None, [], IN_KERNEL),  # balanced, B=2
     ([4096] * 8, 32, 8, 128, torch.float16, None, [], IN_KERNEL),  # balanced, units split 4 ways
     ([65536] + [1024] * 15, 32, 8, 128, torch.float16, None, [], IN_KERNEL),  # skewed, balanced
     ("r24", 64, 8, 128, torch.bfloat16, None, [3, 17], IN_KERNEL),  # G=8, empty sequences
@@ -63,8 +64,11 @@ CASES = [
     ("m64", 32, 1, 128, torch.bfloat16, None, [9], MERGE_KERNEL),  # MQA: 32-head units, balanced
     ([6000, 30, 2500, 800], 32, 1, 64, torch.float16, 7, [], MERGE_KERNEL),  # MQA, uniform splits, head_dim 64
     ([3000] * 4, 96, 4, 128, torch.float16, None, [], MERGE_KERNEL),  # 24 heads per unit (two head tiles)
-    ([32768], 8, 1, 128, torch.float16, None, [], MERGE_KERNEL),  # one unit over 256 workgroups
-    ([2048], 8, 1, 128, torch.float16, None, [], IN_KERNEL),  # one unit over 16 workgroups
+    ([32768], 8, 1, 128, torch.float16, None, [], MERGE_KERNEL),  # one unit over 64 splits
+    ([2048], 8, 1, 128, torch.float16, None, [], MERGE_KERNEL),  # 16 splits, two heads per wave
+    ([1024], 8, 1, 128, torch.float16, None, [], IN_KERNEL),  # 8 splits, two heads per wave
+    ([4096, 4000], 32, 8, 128, torch.float16, None, [], IN_KERNEL),  # balanced, 16 workgroups per unit
+    ([4096, 4000], 64, 8, 128, torch.bfloat16, None, [], MERGE_KERNEL),  # the same, two heads per wave
 ]
 
 
