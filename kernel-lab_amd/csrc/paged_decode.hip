@@ -70,6 +70,8 @@ constexpr int kMaxPlannedSplits = 64;
 constexpr int kMinPagesPerSplit = 16;      // fewest pages a planned uniform split takes
 constexpr int kMinPagesPerSingleSplit = 8;  // the same for a batch of one sequence
 constexpr int kMinPagesPerBalancedWg = 8;  // fewest pages a balanced-schedule workgroup takes
+constexpr int kFusedMaxSegments = 8;       // most segments of a balanced unit merged in the kernel
+constexpr int kMinSegmentPages = 32;       // ... while its segments are shorter than this (make_plan)
 // Cache policy of the K/V loads: streamed once, so non-temporal. Measured on
 // 32/8/128 fp16 B=64 ctx 4096: nt 173 us, nt with sc0 and/or sc1 172.5-173.7,
 // no policy bits 221.
@@ -2259,8 +2261,21 @@ int make_plan(const Options& opt, kl_dtype dtype, int batch, int num_q_heads, in
     // At most kMaxPlannedSplits workgroups per list unit, as for uniform
     // splits: 8/1/128 fp16 B=2 ctx 32768 took 22.1 us as 256 workgroups (128
     // per sequence) and 17.2 us as 64 uniform splits.
-    const int64_t grid = std::max<int64_t>(
+    int64_t grid = std::max<int64_t>(
         1, std::min<int64_t>({cdiv(upper, kMinPagesPerBalancedWg), floor_wgs, lunits * kMaxPlannedSplits, 0x7fffffffLL}));
+    // Units merged in the kernel are cut into at most kFusedMaxSegments
+    // segments while a full sequence's segments would stay under 32 pages and
+    // the cut still gives at least half the CUs a workgroup. Measured on
+    // MI355X (events, us, 256 workgroups -> the cut): 32/8/128 fp16 B=2 ctx
+    // 2048 14.98 -> 13.56, ctx 4096 17.08 -> 16.40, B=3 ctx 2048 17.12 ->
+    // 14.38, ctx 4096 20.08 -> 17.82; 64/8/128 bf16 B=3 ctx 4096 21.64 ->
+    // 18.62; 32/4/128 bf16 B=4 ctx 4096 17.82 -> 17.14; longer contexts and
+    // larger batches unchanged, a ragged 3-sequence batch +0.3 us.
+    const int64_t segments = cdiv(grid, lunits);
+    if (!pair_balanced && p->heads_per_wg <= kFusedMergeMaxHeads && segments > kFusedMaxSegments &&
+        lunits * kFusedMaxSegments >= cus / 2 && pages < kMinSegmentPages * segments) {
+      grid = lunits * std::max<int64_t>(kFusedMaxSegments, cdiv(pages, kMinSegmentPages));
+    }
     p->grid = static_cast<int>(grid);
     p->paired = pair_balanced;
     p->num_splits = 0;

@@ -67,8 +67,9 @@ CASES = [
     ([32768], 8, 1, 128, torch.float16, None, [], MERGE_KERNEL),  # one unit over 64 splits
     ([2048], 8, 1, 128, torch.float16, None, [], MERGE_KERNEL),  # 16 splits, two heads per wave
     ([1024], 8, 1, 128, torch.float16, None, [], IN_KERNEL),  # 8 splits, two heads per wave
-    ([4096, 4000], 32, 8, 128, torch.float16, None, [], IN_KERNEL),  # balanced, 16 workgroups per unit
-    ([4096, 4000], 64, 8, 128, torch.bfloat16, None, [], MERGE_KERNEL),  # the same, two heads per wave
+    ([4096, 4000], 32, 8, 128, torch.float16, None, [], IN_KERNEL),  # balanced, 8 short segments per unit
+    ([4096, 4000], 64, 8, 128, torch.bfloat16, None, [], IN_KERNEL),  # the same, two heads per wave
+    ([8192, 8000], 64, 8, 128, torch.bfloat16, None, [], MERGE_KERNEL),  # 16 segments, two heads per wave
 ]
 
 
