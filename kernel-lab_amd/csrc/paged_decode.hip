@@ -2274,7 +2274,7 @@ int make_plan(const Options& opt, kl_dtype dtype, int batch, int num_q_heads, in
     const int64_t segments = cdiv(grid, lunits);
     if (!pair_balanced && p->heads_per_wg <= kFusedMergeMaxHeads && segments > kFusedMaxSegments &&
         lunits * kFusedMaxSegments >= cus / 2 && pages < kMinSegmentPages * segments) {
-      grid = lunits * std::max<int64_t>(kFusedMaxSegments, cdiv(pages, kMinSegmentPages));
+      grid = std::min(grid, lunits * std::max<int64_t>(kFusedMaxSegments, cdiv(pages, kMinSegmentPages)));
     }
     p->grid = static_cast<int>(grid);
     p->paired = pair_balanced;

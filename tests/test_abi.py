@@ -166,6 +166,7 @@ def _align(n: int) -> int:
         (2, 8, 256, False),  # 16 short segments per unit: cut 8 ways instead
         (3, 8, 128, False),
         (2, 8, 512, False),  # 32-page segments: 16 of them
+        (3, 8, 336, False),  # 24 units, 11 segments of 31 pages: never more workgroups than before the cut
     ],
 )
 def test_planner_pairs_long_contexts_of_small_batches(batch, hkv, max_pages, paired):
@@ -180,7 +181,7 @@ def test_planner_pairs_long_contexts_of_small_batches(batch, hkv, max_pages, pai
     grid = min(256, -(-lunits * max_pages // 8), lunits * 64)
     segments = -(-grid // lunits)
     if not paired and segments > 8 and lunits * 8 >= 128 and max_pages < 32 * segments:
-        grid = lunits * max(8, -(-max_pages // 32))  # units merged in the kernel: at most 8 short segments
+        grid = min(grid, lunits * max(8, -(-max_pages // 32)))  # units merged in the kernel: at most 8 short segments
     slots = (grid + lunits) * (2 if paired else 1)
     assert splits == 0
     assert ws == _align(slots * 4 * 128 * 4) + _align(slots * 4 * 4)
