@@ -98,10 +98,11 @@ int kl_rms_norm(kl_dtype dtype, void* out, const void* x, void* residual, const 
  *   cu_count         compute units to plan for; 0 queries the current device
  *   out_num_splits   (host pointer) uniform splits the launch will use, or 0
  *                    when it balances pages across sequences on the device
- *                    (chosen for fp16/bf16 when there are fewer
- *                    (sequence, KV head) units than compute units, or when a
- *                    full batch's table spans >= 256 pages and the balanced
- *                    workspace stays within 16 MiB)
+ *                    (chosen for fp16/bf16 batches of two or more sequences
+ *                    when there are fewer (sequence, KV head) units than
+ *                    compute units, or when a full batch's table spans >= 256
+ *                    pages and the balanced workspace stays within 16 MiB; a
+ *                    single sequence takes uniform splits of >= 8 pages)
  *   out_workspace    (host pointer) bytes of device workspace the launch needs
  *                    (0 when the launch needs none)
  */
