@@ -19,6 +19,7 @@ import torch
 
 from kernel_lab import _native
 from kernel_lab.kv_cache import build_paged_kv, device_decode_problem, random_decode_problem
+from kernel_lab.ops import plan_decode
 from oracle import reference as ref
 from tests.conftest import DTYPES, decode_parity
 
@@ -248,6 +249,29 @@ def test_long_segments_refill_the_block_table_window(gpu_ops, page, dtype, hq, s
     q, kv, _, _ = random_decode_problem(lens, hq, 8, 128, page, dtype=dtype, device="cuda", poison=float("nan"),
                                         seed=page + hq)
     check(run(gpu_ops, q, kv, num_splits=splits), expected(q, kv), dtype, f"page {page} splits {splits}")
+
+
+@pytest.mark.parametrize(
+    ("hq", "hkv", "ctx", "dtype"),
+    [
+        (32, 8, 4096, torch.float16),  # 32 uniform splits, merge kernel
+        (32, 8, 1024, torch.float16),  # 8 splits, merged in the kernel
+        (64, 8, 32768, torch.bfloat16),
+        (8, 1, 32768, torch.float16),  # 64 splits of one KV head
+        (32, 1, 20000, torch.bfloat16),  # two head tiles; the length ends mid-page
+        (32, 4, 8190, torch.float16),
+    ],
+)
+def test_single_sequence_uniform_splits(gpu_ops, hq, hkv, ctx, dtype):
+    """A batch of one sequence takes uniform splits of >= 8 pages (it cannot be
+    skewed); many-way splits at long contexts, checked against the unrounded
+    oracle, with NaN in every unused page."""
+    q, kv, _, _ = random_decode_problem([ctx], hq, hkv, 128, 16, dtype=dtype, device="cuda", poison=float("nan"),
+                                        seed=ctx + hq)
+    pages = kv.block_table.shape[1]
+    splits, _ = plan_decode(dtype, 1, hq, hkv, 128, 16, pages, 0)
+    assert splits > 1 and -(-pages // splits) >= 8, (splits, pages)  # uniform (0 would be the balanced schedule)
+    check(run(gpu_ops, q, kv), expected(q, kv), dtype, f"{hq}/{hkv} ctx {ctx} splits {splits}")
 
 
 def test_config4_long_context_gqa(gpu_ops):
