@@ -100,9 +100,13 @@ int kl_rms_norm(kl_dtype dtype, void* out, const void* x, void* residual, const 
  *                    when it balances pages across sequences on the device
  *                    (chosen for fp16/bf16 batches of two or more sequences
  *                    when there are fewer (sequence, KV head) units than
- *                    compute units, or when a full batch's table spans >= 256
- *                    pages and the balanced workspace stays within 16 MiB; a
- *                    single sequence takes uniform splits of >= 8 pages)
+ *                    compute units, and for full batches while the balanced
+ *                    workspace stays within 16 MiB: one workgroup per unit,
+ *                    which on an even batch is one uniform split's cut,
+ *                    detected on the device; full batches of more than 8
+ *                    query heads per KV head take it only when the table
+ *                    spans >= 256 pages; a single sequence takes uniform
+ *                    splits of >= 8 pages)
  *   out_workspace    (host pointer) bytes of device workspace the launch needs
  *                    (0 when the launch needs none)
  */
@@ -176,9 +180,7 @@ int kl_paged_decode_reload_options(void);
 /*
  * kl_paged_decode_attention without a workspace argument, for callers that
  * cannot allocate device memory (code under HIP graph capture, serving loops
- * that forbid allocation). No counterpart exists in the reference: its
- * launchers need no split workspace, and its Triton wrapper allocates one per
- * call (kernel_lab/triton_kernels/paged_attention.py:213-214).
+ * that forbid allocation). It has no counterpart in the reference.
  *
  * The split workspace lives in a library-owned 16 MiB device array, one per
  * device, held until the process ends; it fits every split the planner

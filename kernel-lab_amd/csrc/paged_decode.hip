@@ -85,9 +85,10 @@ constexpr int kKvPolicy = kCachePolicyNT;
 // splits to the merge (64/8/128 B=1 ctx 32768, 64 segments: +6 us).
 constexpr int kPairMinPages = 128;
 constexpr int kPairMaxSegments = 16;
-// Full batches take the balanced schedule from this many block-table columns
-// on (see make_plan), as long as its workspace stays within
-// kAutoBalanceMaxWorkspace (the no-allocation entry point's array).
+// Full batches take the balanced schedule by default as long as its
+// workspace stays within kAutoBalanceMaxWorkspace (the no-allocation entry
+// point's array); those whose split units would need the separate merge
+// launch only from this many block-table columns on (see make_plan).
 constexpr int kBalanceMinPages = 256;
 constexpr size_t kAutoBalanceMaxWorkspace = size_t{16} << 20;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -126,6 +127,10 @@ struct DecodeArgs {
   int head_groups;      // workgroups per (sequence, KV head, split) along the group
   int heads_per_wg;     // query heads one workgroup handles
   int grid;             // workgroups of the balanced decode kernel (0: uniform splits)
+  // Balanced kernel: 1 when the grid is one workgroup per list unit and the
+  // batch has at most 64 * kScanChunks sequences, else 0 (see
+  // decode_mfma_balanced_kernel's even-batch start).
+  int even_start;
   float scale_log2;     // scale * log2(e)
   // Query-row mapping. Local head hl of KV head kvh in sequence b reads q row
   // (b + hl / q_fold) * q_heads + kvh * q_fold + hl % q_fold, and the output
@@ -354,7 +359,8 @@ __device__ __forceinline__ void fetch_args(const DecodeArgs& a) {
                "s"(a.lse_part), "s"(a.bt_stride), "s"(a.page_stride), "s"(a.arrivals));
   asm volatile("" ::"s"(a.token_stride), "s"(a.batch), "s"(a.num_q_heads), "s"(a.num_kv_heads), "s"(a.group),
                "s"(a.page_size), "s"(a.bpp_magic), "s"(a.bpp_shift), "s"(a.max_pages), "s"(a.num_splits),
-               "s"(a.pages_per_split), "s"(a.head_groups), "s"(a.heads_per_wg), "s"(a.grid), "s"(a.scale_log2),
+               "s"(a.pages_per_split), "s"(a.head_groups), "s"(a.heads_per_wg), "s"(a.grid), "s"(a.even_start),
+               "s"(a.scale_log2),
                "s"(a.q_fold), "s"(a.q_heads), "s"(a.force_partial));
 }
 
@@ -1242,7 +1248,64 @@ __device__ __forceinline__ int pages_of(const DecodeArgs& a, int len) {
   return len > 0 ? (len + a.page_size - 1) / a.page_size : 0;
 }
 
-__device__ __forceinline__ Start schedule_start(const DecodeArgs& a, int units_per_seq, int wg) {
+// seq_lens of a batch of at most 64 * kScanChunks sequences: lane l of chunk
+// k holds sequence 64k + l (0 past the batch). All chunks' loads are issued
+// before any is used, through a resource that ends with the array, so lanes
+// past the batch read 0 with no branch. (A per-lane branch around each load,
+// with its clamp inside, made the compiler wait for each load in turn: one
+// memory round trip per 64 sequences.) Chunks past the batch are skipped by
+// uniform branches.
+struct LenChunks {
+  int raw[kScanChunks];
+};
+
+__device__ __forceinline__ LenChunks load_len_chunks(const DecodeArgs& a) {
+  const int lane = __lane_id();
+  const auto lens_rsrc = make_rsrc_bytes(uniform_ptr(a.seq_lens), static_cast<uint32_t>(a.batch) * 4u);
+  LenChunks c;
+#pragma unroll
+  for (int k = 0; k < kScanChunks; ++k) {
+    c.raw[k] = 0;
+    if (64 * k < a.batch) {
+      c.raw[k] = __builtin_bit_cast(int, buffer_load_f32(lens_rsrc, static_cast<uint32_t>((64 * k + lane) * 4)));
+    }
+  }
+  return c;
+}
+
+// The page count every sequence of the batch has (batch <= 64 *
+// kScanChunks), or 0 when two sequences differ or sequence 0 has no page.
+// One compare per lane and chunk: a length has n pages exactly when it lies
+// in ((n - 1) * page_size, n * page_size].
+__device__ __forceinline__ int even_pages(const DecodeArgs& a, const LenChunks& c) {
+  const int lane = __lane_id();
+  const int n = pages_of(a, clamped_len(a, __builtin_amdgcn_readfirstlane(c.raw[0])));
+  const int64_t lo = static_cast<int64_t>(n - 1) * a.page_size;  // exclusive
+  const int64_t hi = static_cast<int64_t>(n) * a.page_size;
+  bool differ = false;
+#pragma unroll
+  for (int k = 0; k < kScanChunks; ++k) {
+    if (64 * k < a.batch) {
+      const int len = clamped_len(a, c.raw[k]);
+      differ |= 64 * k + lane < a.batch && (len <= lo || len > hi);
+    }
+  }
+  return n > 0 && __ballot(differ) == 0 ? n : 0;
+}
+
+// The clamped length of sequence b (wave-uniform, b < batch <= 64 *
+// kScanChunks), read from the lanes that loaded it.
+__device__ __forceinline__ int chunk_len(const DecodeArgs& a, const LenChunks& c, int b) {
+  int raw = 0;
+#pragma unroll
+  for (int k = 0; k < kScanChunks; ++k) {
+    if ((b >> 6) == k) raw = __builtin_amdgcn_readlane(c.raw[k], b & 63);
+  }
+  return clamped_len(a, raw);
+}
+
+// c: the batch's seq_lens (load_len_chunks) when batch <= 64 * kScanChunks.
+__device__ __forceinline__ Start schedule_start(const DecodeArgs& a, int units_per_seq, int wg, const LenChunks& c) {
   const int lane = __lane_id();
   Start s;
 #pragma unroll
@@ -1252,23 +1315,8 @@ __device__ __forceinline__ Start schedule_start(const DecodeArgs& a, int units_p
   if (a.batch <= 64 * kScanChunks) {
     int len[kScanChunks], pl[kScanChunks], incl[kScanChunks];
     int64_t before[kScanChunks];
-    // All chunks' seq_lens loads are issued before any is used, through a
-    // resource that ends with the array: lanes past the batch read 0 with no
-    // branch. (A per-lane branch around each load, with its clamp inside,
-    // made the compiler wait for each load in turn: one memory round trip
-    // per 64 sequences.) Chunks past the batch are skipped by uniform
-    // branches: a scan is a chain of cross-lane steps, not free.
-    const auto lens_rsrc = make_rsrc_bytes(uniform_ptr(a.seq_lens), static_cast<uint32_t>(a.batch) * 4u);
-    int raw[kScanChunks];
 #pragma unroll
-    for (int k = 0; k < kScanChunks; ++k) {
-      raw[k] = 0;
-      if (64 * k < a.batch) {
-        raw[k] = __builtin_bit_cast(int, buffer_load_f32(lens_rsrc, static_cast<uint32_t>((64 * k + lane) * 4)));
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < kScanChunks; ++k) len[k] = clamped_len(a, raw[k]);
+    for (int k = 0; k < kScanChunks; ++k) len[k] = clamped_len(a, c.raw[k]);
     int64_t total = 0;
 #pragma unroll
     for (int k = 0; k < kScanChunks; ++k) {
@@ -1358,6 +1406,21 @@ __device__ __forceinline__ int paired_list_wg(const DecodeArgs& a, int units_per
   return (i % rows) * m + i / rows;
 }
 
+// The unit of list unit ui (hp list units per sequence; KV heads PAIR * j +
+// half for list unit j of a sequence's hp), wave-uniform.
+template <int PAIR>
+__device__ __forceinline__ Unit list_unit(const DecodeArgs& a, int hp, int ui, int half) {
+  const int b = ui / hp;
+  const int r = ui - b * hp;
+  const int rkv = a.head_groups == 1 ? r : r / a.head_groups;
+  Unit u;
+  u.b = __builtin_amdgcn_readfirstlane(b);
+  u.kvh = __builtin_amdgcn_readfirstlane(rkv * PAIR + half);
+  u.hg = __builtin_amdgcn_readfirstlane(r - rkv * a.head_groups);
+  u.split = 0;
+  return u;
+}
+
 // PAIR = 2 (num_kv_heads even): the work list's units are KV-head pairs (j,
 // head group); the workgroup has two halves of W waves that walk the same
 // segments, half h streaming KV head 2j + h with its own LDS (adjacent bytes
@@ -1375,7 +1438,43 @@ __global__ void __launch_bounds__(PAIR * kThreads, (mfma_waves_per_eu<D, NT>()))
   const int half = PAIR == 2 ? wave_id() / W : 0;
   const int hp = a.num_kv_heads * a.head_groups / PAIR;  // list units per sequence
   const int w = PAIR == 2 ? paired_list_wg(a, hp) : static_cast<int>(blockIdx.x);
-  const Start st = schedule_start(a, hp, w);
+  const int hw = wave_id() - half * W;  // wave within the half
+  // Even-batch start. When the grid is one workgroup per list unit
+  // (even_start) and every sequence has the same page count n >=
+  // kMinPagesPerBalancedWg, workgroup w's range is exactly list unit w,
+  // whole: the uniform cut. For that case the unit's first block-table
+  // window, then seq_lens, then its q are issued before any of them is
+  // waited for, as the uniform kernels issue theirs, and the scan is
+  // skipped; any other batch runs the schedule below, after the guessed
+  // loads land. The order is measured: with q issued before the window
+  // (the uniform kernels' order), the whole kernel ran 12-16 % slower on
+  // MI355X (32/8/128 fp16 B=64 ctx 4096 187 vs 162 us, ragged 228 vs 205),
+  // on the guessed path and on the scan after a failed guess alike, though
+  // the main loops compiled to the same instructions; q after the window
+  // and seq_lens costs nothing measurable.
+  Unit gu{};
+  QFrag<NT, D / 32> gq;
+  if (a.even_start) {
+    gu = list_unit<PAIR>(a, hp, w, half);
+    prefetch_window<KVF, D, NT>(a, lds + half * Lds::kBytes, gu.b, 0, a.max_pages, hw);
+  }
+  LenChunks lc;
+  if (a.batch <= 64 * kScanChunks) lc = load_len_chunks(a);
+  if (a.even_start) {
+    load_q<E, D, NT>(a, gu, gq);
+    const int n = even_pages(a, lc);
+    if (n >= kMinPagesPerBalancedWg) {
+      gu.seq_len = __builtin_amdgcn_readfirstlane(chunk_len(a, lc, gu.b));
+      gu.page_begin = 0;
+      gu.page_end = n;
+      Dest dst{};
+      dst.final = true;
+      mfma_segment<E, KVF, D, NT, W>(a, lds + half * Lds::kBytes, gu, dst, hw, &gq, true);
+      return;
+    }
+    wait_vmcnt<0>();  // the guessed window loads write LDS the segments below reuse
+  }
+  const Start st = schedule_start(a, hp, w, lc);
   if (a.arrivals != nullptr) {
     // No merge kernel follows: empty sequences get their zeros here, sequence
     // b from workgroup b % grid (up to 64 * kScanChunks from the schedule's scan).
@@ -1437,7 +1536,7 @@ __global__ void __launch_bounds__(PAIR * kThreads, (mfma_waves_per_eu<D, NT>()))
     // The previous segment's waves may still read LDS; before the first
     // segment nothing has used it (the schedule needs no LDS), so no barrier.
     if (pos != st.pos) __syncthreads();
-    mfma_segment<E, KVF, D, NT, W>(a, lds + half * Lds::kBytes, u, dst, wave_id() - half * W);
+    mfma_segment<E, KVF, D, NT, W>(a, lds + half * Lds::kBytes, u, dst, hw);
     if (NT == 1 && !dst.final && a.arrivals != nullptr) {  // see kFusedMergeMaxHeads
       // The unit's segments are workgroups w0 .. w1 (slots (w + list unit) * PAIR + half).
       const int64_t w0 = unit_base / st.per;
@@ -1456,7 +1555,7 @@ __global__ void __launch_bounds__(PAIR * kThreads, (mfma_waves_per_eu<D, NT>()))
       job.out = static_cast<typename E::S*>(a.out) +
                 (static_cast<int64_t>(u.b) * a.num_q_heads + u.kvh * a.group + h0) * D;
       const int64_t unit = (static_cast<int64_t>(u.b) * a.num_kv_heads + u.kvh) * a.head_groups + u.hg;
-      arrive_and_merge<E, W>(a.arrivals + unit, job, D, wave_id() - half * W, s_last + half);
+      arrive_and_merge<E, W>(a.arrivals + unit, job, D, hw, s_last + half);
     }
 
     pos = unit_base + page1;
@@ -2025,6 +2124,24 @@ Options options() {
   return o;
 }
 
+// Device address of a file-scope __device__ array on the current device.
+// The lookup is not a stream operation, but the first one may load the code
+// object, a call the runtime can refuse while any thread captures a graph in
+// the global mode (torch.cuda.graph's default); this thread's capture mode is
+// relaxed for the lookup and restored after it.
+template <typename T>
+hipError_t device_symbol_address(void** p, const T& symbol) {
+  hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+  const bool swapped = hipThreadExchangeStreamCaptureMode(&mode) == hipSuccess;
+  const hipError_t err = hipGetSymbolAddress(p, reinterpret_cast<const void*>(&symbol));
+  if (swapped) {
+    (void)hipThreadExchangeStreamCaptureMode(&mode);
+  } else {
+    (void)hipGetLastError();  // the failed exchange must not reach the launch check
+  }
+  return err;
+}
+
 // The arrival-counter region for a fused call on `stream` (current device),
 // or null for the merge kernel.
 //   eager stream      the stream's own region, taken on its first fused call
@@ -2091,7 +2208,7 @@ uint32_t* arrival_region(hipStream_t stream) {
     void* p = nullptr;
     // The device array's own name is a host-side stand-in: its device address
     // comes from the runtime, once per device.
-    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_decode_arrivals)) == hipSuccess) {
+    if (device_symbol_address(&p, g_decode_arrivals) == hipSuccess) {
       d.base = static_cast<uint32_t*>(p);
     } else {
       (void)hipGetLastError();  // the merge kernel serves this device; the launch check must not see this error
@@ -2225,18 +2342,22 @@ int make_plan(const Options& opt, kl_dtype dtype, int batch, int num_q_heads, in
                           pair_units * kPairMaxSegments >= cus;
   const bool pairable = mfma && !partials && opt.pairing() && num_kv_heads % 2 == 0 && head_dim <= 128 &&
                         p->heads_per_wg <= 16 && (units >= 2 * static_cast<int64_t>(cus) || long_pairs);
-  // For batches whose units fill the device (units >= CUs) the choice is the
-  // balanced schedule when the block table is long (kBalanceMinPages or more
-  // columns) and uniform splits otherwise. The planner cannot see seq_lens,
-  // and with uniform splits one long sequence among short ones sets the time:
-  // measured on MI355X (events, us, same tensors alternating), one
-  // 65,536-token sequence among 63 of 2,048 tokens 1,231 (uniform) vs 142
-  // (balanced), ragged U[1, 8192] B=64 228 vs 207. On an even batch the
-  // balanced schedule gives every workgroup the same single unit and costs
-  // only its start: 163.4 vs 164.6 (32/8/128 fp16 B=64 ctx 4096), but on
-  // short tables that start weighs more (B=32 ctx 512 19.0 vs 19.9, B=128
-  // ctx 2048 169.0 vs 174.2) while the worst skew costs less.
-  const int full_batch_choice = opt.balance();  // 1 balanced, 0 uniform, -1 by table length
+  // Batches whose units fill the device (units >= CUs) take the balanced
+  // schedule too. The planner cannot see seq_lens, and with uniform splits
+  // one long sequence among short ones sets the time: measured on MI355X
+  // (events, us, same tensors alternating), one 65,536-token sequence among
+  // 63 of 2,048 tokens 1,231 (uniform) vs 142 (balanced), ragged U[1, 8192]
+  // B=64 228 vs 207. A full batch gets one workgroup per list unit, so on an
+  // even batch each workgroup's range is one whole unit, the uniform cut,
+  // and the kernel starts it as the uniform kernels do (its even-batch
+  // start); the choice between the two cuts is made on the device. Where a
+  // split unit would need the separate merge launch (more than
+  // kFusedMergeMaxHeads query heads per workgroup, or the fused merge
+  // switched off), short tables keep uniform splits: that launch costs more
+  // than a short table's worst skew.
+  const int full_batch_choice = opt.balance();  // 1 balanced, 0 uniform, -1 by default
+  const bool full_default =
+      (p->heads_per_wg <= kFusedMergeMaxHeads && opt.fused_merge()) || pages >= kBalanceMinPages;
   const bool requested = num_splits == KL_SPLITS_BALANCED;
   // One sequence cannot be skewed: uniform splits cut it as evenly as the
   // balanced schedule would, without its start (the seq_lens scan before the
@@ -2247,11 +2368,12 @@ int make_plan(const Options& opt, kl_dtype dtype, int batch, int num_q_heads, in
   const bool single = batch == 1 && !long_pairs;
   const bool automatic =
       num_splits == 0 && !single &&
-      (units < cus || (full_batch_choice < 0 ? pages >= kBalanceMinPages : full_batch_choice == 1));
+      (units < cus || (full_batch_choice < 0 ? full_default : full_batch_choice == 1));
   const bool balance = requested || automatic;
   const bool pair_balanced = pairable && balance;
   if (mfma && !partials && balance) {
-    // Requested, or fewer units than CUs: pages balanced across sequences on the device.
+    // Requested, fewer units than CUs, or a full batch by default: pages
+    // balanced across sequences on the device.
     const int64_t lunits = pair_balanced ? units / 2 : units;  // units of the work list
     const int64_t upper = lunits * pages;                        // list length if every sequence were full
     // Paired: one 8-wave workgroup per CU is the register budget, so more
@@ -2276,17 +2398,30 @@ int make_plan(const Options& opt, kl_dtype dtype, int batch, int num_q_heads, in
         lunits * kFusedMaxSegments >= cus / 2 && pages < kMinSegmentPages * segments) {
       grid = std::min(grid, lunits * std::max<int64_t>(kFusedMaxSegments, cdiv(pages, kMinSegmentPages)));
     }
-    p->grid = static_cast<int>(grid);
+    // Workspace: a partial slot per workgroup and list unit (two when paired).
+    auto set_grid = [&](int64_t g) {
+      p->grid = static_cast<int>(g);
+      const size_t slots = (static_cast<size_t>(g) + static_cast<size_t>(lunits)) * (pair_balanced ? 2 : 1);
+      p->o_bytes = align_up(slots * p->heads_per_wg * head_dim * sizeof(float));
+      p->ws_bytes = p->o_bytes + align_up(slots * p->heads_per_wg * sizeof(float));
+    };
+    set_grid(grid);
+    if (units >= cus && lunits >= cus) {
+      // A full batch: one workgroup per list unit (the uniform cut on an even
+      // batch) when that still gives every CU a workgroup, unless that
+      // workspace would be large.
+      const int64_t each = std::max<int64_t>(1, std::min<int64_t>(lunits, cdiv(upper, kMinPagesPerBalancedWg)));
+      const Plan keep = *p;
+      set_grid(each);
+      if (p->ws_bytes > kAutoBalanceMaxWorkspace) *p = keep;
+    }
     p->paired = pair_balanced;
     p->num_splits = 0;
     p->pages_per_split = 0;
-    const size_t slots = (static_cast<size_t>(grid) + static_cast<size_t>(lunits)) * (pair_balanced ? 2 : 1);
-    p->o_bytes = align_up(slots * p->heads_per_wg * head_dim * sizeof(float));
-    p->ws_bytes = p->o_bytes + align_up(slots * p->heads_per_wg * sizeof(float));
-    // A full batch chosen by table length keeps uniform splits when the
-    // balanced workspace (a slot per workgroup and unit) would be large.
-    const bool by_length = !requested && units >= cus && full_batch_choice < 0;
-    if (!by_length || p->ws_bytes <= kAutoBalanceMaxWorkspace) return ok();
+    // A full batch balanced by default keeps uniform splits when the balanced
+    // workspace would be large.
+    const bool by_default = !requested && units >= cus && full_batch_choice < 0;
+    if (!by_default || p->ws_bytes <= kAutoBalanceMaxWorkspace) return ok();
     p->grid = 0;
     p->paired = false;
   }
@@ -2447,7 +2582,12 @@ int launch_uniform_mfma(const DecodeArgs& a, int head_dim, unsigned grid, hipStr
 template <typename E, typename KVF>
 int launch_balanced(DecodeArgs a, int head_dim, hipStream_t stream) {
   const unsigned grid = static_cast<unsigned>(a.grid);
-  a.arrivals = fused_merge_counters(a, static_cast<int64_t>(a.batch) * a.num_kv_heads * a.head_groups, stream);
+  const int64_t units = static_cast<int64_t>(a.batch) * a.num_kv_heads * a.head_groups;
+  // The even-batch start needs one workgroup per list unit and the batch's
+  // seq_lens in one wave-wide scan.
+  const int64_t lunits = a.paired ? units / 2 : units;
+  a.even_start = a.grid == lunits && a.batch <= 64 * kScanChunks ? 1 : 0;
+  a.arrivals = fused_merge_counters(a, units, stream);
   int st = dispatch_mfma(head_dim, a.heads_per_wg, [&](auto d, auto nt) -> int {
     constexpr int D = decltype(d)::value, NT = decltype(nt)::value;
     if constexpr (mfma_instance_exists<KVF, D>()) {
@@ -2600,6 +2740,7 @@ int decode_entry(kl_dtype dtype, bool kv8, void* out, const void* q, const void*
   a.pages_per_split = p.pages_per_split;
   a.head_groups = p.head_groups;
   a.grid = p.grid;
+  a.even_start = 0;  // set by launch_balanced
   a.heads_per_wg = p.heads_per_wg;
   a.scale_log2 = scale * kLog2e;
   a.q_fold = a.group;
@@ -2647,8 +2788,10 @@ extern "C" int kl_paged_decode_reload_options(void) {
 // The split workspace of kl_paged_decode_attention (fp32 partial outputs and
 // their log2-sum-exps) for callers that cannot allocate device memory, in a
 // library-owned array. 16 MiB holds every split the planner chooses by itself
-// (num_splits 0): at most about 8.5 MB, 511 balanced slots of 32 heads x 129
-// floats or 16 heads x 257. Each device holds its own copy until the process
+// (num_splits 0): the planner keeps a full batch's balanced workspace within
+// kAutoBalanceMaxWorkspace (this size) and falls back to uniform splits
+// beyond it; smaller batches need at most about 8.5 MB (511 balanced slots of
+// 32 heads x 129 floats or 16 heads x 257). Each device holds its own copy until the process
 // ends. No byte of it has to start at zero: a merge reads only partials that
 // the same call wrote before. Calls that overlap on one device share it, so
 // they race.
@@ -2680,7 +2823,7 @@ void* scratch_for_current_device() {
   std::lock_guard<std::mutex> lock(mu);
   if (addr[dev] == nullptr) {
     void* p = nullptr;
-    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    const hipError_t err = device_symbol_address(&p, scratch);
     if (err != hipSuccess) {
       fail_hip(err, "hipGetSymbolAddress(scratch)");
       return nullptr;
@@ -2700,6 +2843,8 @@ extern "C" int kl_paged_decode_attention_noalloc(kl_dtype dtype, void* out, cons
                                                  int64_t block_table_stride, int max_pages, float scale,
                                                  int num_splits, kl_stream_t stream) {
   using namespace kl;
+  // Every return below, including a refusal, reports no merge.
+  g_last_merge = KL_MERGE_NONE;
   // Set-up first: the device's scratch address is looked up on the first call
   // on each device, whatever this call needs.
   void* ws = scratch_for_current_device();

@@ -96,29 +96,43 @@ def test_planner_fills_the_device(batch, hkv, max_pages, cus, want):
 
 
 @pytest.mark.parametrize(
-    ("batch", "hkv", "max_pages", "balanced"),
+    ("batch", "hkv", "hq", "max_pages", "balanced"),
     [
-        (64, 8, 255, False),  # full batch, short table: one uniform split
-        (32, 8, 128, False),
-        (64, 8, 256, True),  # full batch, long table: balanced (one long sequence cannot stall it)
-        (32, 8, 4096, True),
-        (1024, 16, 8192, False),  # balanced workspace would exceed 16 MiB: uniform
-        (8, 8, 256, True),  # fewer units than CUs: balanced at any table length
-        (2, 8, 32, True),
-        (64, 1, 512, True),
-        (1, 8, 32, False),  # one sequence cannot be skewed: uniform splits
-        (1, 1, 2048, False),
+        (64, 8, 32, 255, True),  # full batch, short table: balanced (the even cut is decided on the device)
+        (32, 8, 32, 128, True),
+        (64, 8, 32, 256, True),
+        (256, 8, 32, 64, True),
+        (32, 8, 32, 4096, True),  # 128 pair units: one 8-wave workgroup per CU, two segments each
+        (64, 8, 128, 255, False),  # 16 heads per workgroup: split units need the merge launch; short table: uniform
+        (64, 8, 128, 256, True),  # ... long table: balanced
+        (1024, 16, 64, 8192, False),  # balanced workspace would exceed 16 MiB: uniform
+        (8, 8, 32, 256, True),  # fewer units than CUs: balanced at any table length
+        (2, 8, 32, 32, True),
+        (64, 1, 4, 512, True),
+        (1, 8, 32, 32, False),  # one sequence cannot be skewed: uniform splits
+        (1, 1, 4, 2048, False),
     ],
 )
-def test_planner_balances_uneven_batches_by_default(batch, hkv, max_pages, balanced):
+def test_planner_balances_uneven_batches_by_default(batch, hkv, hq, max_pages, balanced):
     """fp16/bf16: pages are balanced across sequences on the device (reported
-    as 0 splits, with a workspace of partial slots) when the units do not fill
-    the device, and on full batches whose block table spans >= 256 pages,
-    where one long sequence among short ones would otherwise set the time;
-    full batches with shorter tables take one uniform split."""
-    splits, ws = ops.plan_decode(torch.float16, batch, hkv * 4, hkv, 128, 16, max_pages, 0, 256)
+    as 0 splits, with a workspace of partial slots) when the units do not
+    fill the device, and on full batches, where one long sequence among short
+    ones would otherwise set the time. A full batch gets one workgroup per
+    list unit: on an even batch that is one uniform split's cut, which the
+    kernel detects from seq_lens. Full batches whose split units could not be
+    merged in the kernel (more than 8 query heads per workgroup) keep one
+    uniform split on short tables."""
+    splits, ws = ops.plan_decode(torch.float16, batch, hq, hkv, 128, 16, max_pages, 0, 256)
     if balanced:
         assert splits == 0 and 0 < ws <= 16 << 20
+        units = batch * hkv  # one head group: at most 16 query heads per KV head here
+        paired = hkv % 2 == 0 and (units >= 512 or units // 2 * max_pages >= 256 * 128 and units // 2 * 16 >= 256)
+        lunits = units // 2 if paired else units
+        if units >= 256 and lunits >= 256:  # one workgroup per list unit, a slot per workgroup and unit
+            grid = min(lunits, -(-lunits * max_pages // 8))
+            slots = (grid + lunits) * (2 if paired else 1)
+            heads = min(hq // hkv, 16)
+            assert ws == _align(slots * heads * 128 * 4) + _align(slots * heads * 4)
     elif batch == 1:
         # The uniform rule with >= 8 pages per split, at most 64 splits.
         assert splits == min(-(-256 // hkv), -(-max_pages // 8), 64) and ws > 0
@@ -130,17 +144,18 @@ def test_planner_balances_uneven_batches_by_default(batch, hkv, max_pages, balan
 def test_balanced_planner_on_request(batch, hkv, max_pages):
     """KL_DECODE_BALANCE_ALWAYS=1 gives every fp16/bf16 batch the balanced
     schedule. With an even KV head count and units >= 2 x CUs the list runs in
-    KV-head pairs (one 8-wave workgroup per CU), with a partial slot per half."""
+    KV-head pairs, with a partial slot per half; a full batch gets one
+    workgroup per list unit."""
     with _native.decode_switches(balance_always="1"):
         splits, ws = ops.plan_decode(torch.float16, batch, hkv * 4, hkv, 128, 16, max_pages, 0, 256)
     units = batch * hkv
     long_pairs = units // 2 * max_pages >= 256 * 128 and units // 2 * 16 >= 256
     paired = hkv % 2 == 0 and (units >= 512 or long_pairs)
     lunits = units // 2 if paired else units
-    floor = 256 if paired else max(256, units)
+    floor = lunits if units >= 256 and lunits >= 256 else 256 if paired else max(256, units)
     grid = min(floor, -(-lunits * max_pages // 8))
     slots = (grid + lunits) * (2 if paired else 1)
-    assert splits == 0 and ws >= slots * 4 * (128 + 1) * 4
+    assert splits == 0 and ws == _align(slots * 4 * 128 * 4) + _align(slots * 4 * 4)
     with _native.decode_switches(balance_always="0"):
         uniform = ops.plan_decode(torch.float16, batch, hkv * 4, hkv, 128, 16, max_pages, 0, 256)[0]
     assert uniform >= 1 if units >= 256 else uniform == 0  # fewer units than CUs: balanced regardless
@@ -190,7 +205,9 @@ def test_planner_pairs_long_contexts_of_small_batches(batch, hkv, max_pages, pai
 def test_requested_balanced_schedule_at_any_batch():
     """KL_SPLITS_BALANCED (-1) picks the balanced schedule whatever the planner
     default; the VALU path (fp32) takes the planner's uniform splits."""
-    splits, ws = ops.plan_decode(torch.float16, 64, 32, 8, 128, 16, 256, ops.BALANCED, 256)
+    with _native.decode_switches(balance_always="0"):
+        assert ops.plan_decode(torch.float16, 64, 32, 8, 128, 16, 256, 0, 256)[0] == 1
+        splits, ws = ops.plan_decode(torch.float16, 64, 32, 8, 128, 16, 256, ops.BALANCED, 256)
     units = 64 * 8  # paired: 256 workgroups and 256 pair units, two slots each
     assert splits == 0 and ws >= (256 + units // 2) * 2 * 4 * (128 + 1) * 4
     assert ops.plan_decode(torch.float32, 64, 32, 8, 128, 16, 256, ops.BALANCED, 256) == ops.plan_decode(

@@ -25,7 +25,9 @@ int main(void) {
   printf("ok %s\n", kl_status_string(KL_OK));
   /* Planner: pure host arithmetic with an explicit CU count. */
   int st = kl_paged_decode_plan(KL_DTYPE_F16, 64, 32, 8, 128, 16, 128, 0, 256, &splits, &ws);
-  printf("plan64 %d %d %zu\n", st, splits, ws);
+  printf("plan64 %d %d %d\n", st, splits, ws > 0);
+  st = kl_paged_decode_plan(KL_DTYPE_F16, 64, 128, 8, 128, 16, 128, 0, 256, &splits, &ws);
+  printf("plan64g16 %d %d %zu\n", st, splits, ws);
   st = kl_paged_decode_plan(KL_DTYPE_F16, 64, 32, 8, 128, 16, 256, 0, 256, &splits, &ws);
   printf("plan64long %d %d %d\n", st, splits, ws > 0);
   st = kl_paged_decode_plan(KL_DTYPE_F16, 1, 32, 8, 128, 16, 256, 0, 256, &splits, &ws);
@@ -66,8 +68,9 @@ def test_header_compiles_as_c99_and_links(tmp_path):
     got = dict(line.split(" ", 1) for line in out)
     assert int(got["version"]) >= 100
     assert got["ok"] == "success"
-    st, splits, ws = got["plan64"].split()
-    assert st == "0" and splits == "1" and int(ws) == 0  # one uniform split fills the device
+    assert got["plan64"] == "0 0 1"  # a full batch: balanced, the even cut decided on the device
+    st, splits, ws = got["plan64g16"].split()
+    assert st == "0" and splits == "1" and int(ws) == 0  # 16 heads per workgroup, short table: one uniform split
     assert got["plan64long"] == "0 0 1"  # a long table on a full batch: balanced
     assert got["plan1"] == "0 32 1"  # one sequence: 32 uniform splits of 8 pages
     assert got["plan4"] == "0 0 1"  # a few sequences: balanced schedule

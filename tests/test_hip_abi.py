@@ -101,13 +101,16 @@ def test_ops_work_under_torch_compile(gpu_ops):
     torch.testing.assert_close(y.cpu(), ref_y, **tolerance(torch.float16))
 
 
-def test_balanced_request_reaches_the_planner_on_full_batches(gpu_ops):
-    """64 sequences x 8 KV heads fill the device twice over. With
-    KL_DECODE_BALANCE_ALWAYS=1 the planner's own choice is the balanced
-    schedule in KV-head pairs (a workspace, 0 splits); by default (and with
-    =0) it is one uniform split (no workspace), and KL_SPLITS_BALANCED (-1)
-    still gets the balanced schedule, which needs a workspace and is refused
-    without one."""
+def test_full_batches_balance_skew_by_default(gpu_ops):
+    """64 sequences x 8 KV heads fill the device twice over, and one sequence
+    of 4,000 tokens among 63 of 100 (a 250-column table) would leave its
+    units to stream alone under one uniform split. The planner's default is
+    the balanced schedule (0 splits, a workspace), the same plan as
+    KL_SPLITS_BALANCED (-1); KL_DECODE_BALANCE_ALWAYS=0 gives one uniform
+    split. The drop-in operator (the reference's schema, no split argument)
+    then cuts the long sequence's units over several workgroups and merges
+    them in the kernel, matching the oracle; through the C-ABI the balanced
+    plan needs its workspace and is refused without one."""
     lib = _native.core()
     lens = [4000] + [100] * 63
     q, kv, _, _ = random_decode_problem(lens, 32, 8, 128, 16, dtype=torch.float16, device="cuda", poison=float("nan"))
@@ -120,19 +123,24 @@ def test_balanced_request_reaches_the_planner_on_full_batches(gpu_ops):
         assert lib.kl_paged_decode_plan(code, batch, hq, 8, d, 16, max_pages, req, 0, ctypes.byref(splits), ctypes.byref(ws)) == 0
         return splits.value, ws.value
 
-    assert plan(0) == (1, 0)
-    with _native.decode_switches(balance_always="1"):
-        balanced = plan(0)
+    balanced = plan(0)
     assert balanced[0] == 0 and balanced[1] > 0
+    assert plan(-1) == balanced
     with _native.decode_switches(balance_always="0"):
-        sizes = {0: plan(0), -1: plan(-1)}
-    assert sizes[0] == (1, 0) and sizes[-1] == balanced
+        assert plan(0) == (1, 0)
+    want = ref.paged_decode_attention(q.cpu().float(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table.cpu(), kv.seq_lens.cpu())
+
+    out = torch.full_like(q, float("nan"))
+    torch.ops.kernel_lab.paged_decode_attention(out, q, kv.k_cache, kv.v_cache, kv.block_table, kv.seq_lens, d**-0.5)
+    assert lib.kl_paged_decode_last_merge() == 2, "the long sequence's units should be split and merged in the kernel"
+    torch.cuda.synchronize()
+    decode_parity(out.cpu(), want, torch.float16, "drop-in operator, 1x4000 + 63x100")
+
     out = torch.empty_like(q)
     args = [code, out.data_ptr(), q.data_ptr(), kv.k_cache.data_ptr(), kv.v_cache.data_ptr(), kv.block_table.data_ptr(),
-            kv.seq_lens.data_ptr(), batch, hq, 8, d, 16, kv.block_table.stride(0), max_pages, d**-0.5, -1]
+            kv.seq_lens.data_ptr(), batch, hq, 8, d, 16, kv.block_table.stride(0), max_pages, d**-0.5, 0]
     assert lib.kl_paged_decode_attention(*args, None, 0, stream_handle()) == 3
-    workspace = torch.empty(sizes[-1][1], dtype=torch.uint8, device="cuda")
-    assert lib.kl_paged_decode_attention(*args, workspace.data_ptr(), sizes[-1][1], stream_handle()) == 0
+    workspace = torch.empty(balanced[1], dtype=torch.uint8, device="cuda")
+    assert lib.kl_paged_decode_attention(*args, workspace.data_ptr(), balanced[1], stream_handle()) == 0
     torch.cuda.synchronize()
-    want = ref.paged_decode_attention(q.cpu().float(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table.cpu(), kv.seq_lens.cpu())
-    decode_parity(out.cpu(), want, torch.float16)
+    decode_parity(out.cpu(), want, torch.float16, "C-ABI, planner's choice")

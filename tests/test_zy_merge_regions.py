@@ -7,6 +7,7 @@ merge kernel, with the same bits, and the library says so once on stderr;
 the per-thread default stream (one handle, many streams) never gets a region.
 
 Named to sort late: it takes every eager region for the rest of the process.
+Its checks hold whatever regions earlier tests in the process already took.
 """
 
 from __future__ import annotations
@@ -27,8 +28,12 @@ HIP_STREAM_PER_THREAD = 2  # hipStreamPerThread
 
 
 def _hip():
-    # The HIP runtime PyTorch loaded (same soname: the loader returns that copy).
-    hip = ctypes.CDLL("libamdhip64.so.7")
+    # The HIP runtime this process already loaded (PyTorch's), found by path in
+    # the process's mappings rather than by a fixed soname.
+    with open("/proc/self/maps") as maps:
+        paths = {line.split()[-1] for line in maps if "libamdhip64.so" in line}
+    assert paths, "no HIP runtime mapped in this process"
+    hip = ctypes.CDLL(sorted(paths)[0])
     hip.hipStreamCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
     hip.hipStreamDestroy.argtypes = [ctypes.c_void_p]
     return hip
@@ -60,10 +65,14 @@ def test_streams_beyond_the_regions_take_the_merge_kernel(gpu_ops, capfd):
             hip.hipStreamDestroy(h)
     for i, out in enumerate(outs):
         assert torch.equal(out, want), f"stream {i} (merge {modes[i]}) differs"
-    # Regions go to streams in call order: in-kernel merges, then merge kernels.
-    assert modes[0] == IN_KERNEL and modes[-1] == MERGE_KERNEL, modes
+    # Regions go to streams in call order: in-kernel merges while regions are
+    # left (earlier tests in this process may have taken some), then merge
+    # kernels; 72 new streams outnumber the 64 regions whatever was taken.
+    assert modes[-1] == MERGE_KERNEL, modes
     assert modes == sorted(modes, reverse=True), modes
-    assert capfd.readouterr().err.count("split-merge counter regions for streams are taken") == 1
+    assert set(modes) <= {IN_KERNEL, MERGE_KERNEL}, modes
+    # Said once per process: now, unless an earlier test used the pool up.
+    assert capfd.readouterr().err.count("split-merge counter regions for streams are taken") <= 1
 
 
 def test_per_thread_default_stream_takes_the_merge_kernel(gpu_ops):
