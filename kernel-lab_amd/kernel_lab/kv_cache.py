@@ -68,7 +68,8 @@ def build_paged_kv(
     poison: float = 1e4,
     tail: float = 0.0,
 ) -> PagedKV:
-    """Scatter contiguous per-sequence K/V ([L, Hkv, D] each) into shuffled pages.
+    """Page pools built from each sequence's own K and V ([L, Hkv, D] tensors):
+    the pages are placed at a seeded random permutation of pool slots.
 
     ``extra_pages`` unused pages keep the ``poison`` value: reading one makes
     the result visibly wrong.
@@ -119,7 +120,8 @@ def random_decode_problem(
     poison: float = 1e4,
     tail: float = 0.0,
 ) -> tuple[torch.Tensor, PagedKV, list[torch.Tensor], list[torch.Tensor]]:
-    """A random query batch and its paged cache, plus the contiguous K/V it came from."""
+    """Seeded N(0, 1) queries, keys and values for sequences of the given
+    lengths: returns q, the paged cache, and each sequence's unpaged K and V."""
     generator = torch.Generator().manual_seed(seed)
 
     def rand(*shape: int) -> torch.Tensor:
