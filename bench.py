@@ -24,7 +24,12 @@ Two live passes of K steps each, after W warm-up steps:
 * dominant-kernel pass: K launches of the dominant kernel (decode) back to
   back inside one event pair on the launch stream; per launch this is the
   kernel's duration plus the gap between two launches, and it gives the
-  roofline figure.
+  roofline figure;
+* flushed dominant-kernel pass: K launches of the dominant kernel, each after
+  a read of a 1 GiB buffer (so no input is left in the 256 MB Infinity Cache,
+  and the first K/V loads miss the translation caches as a cold call's do),
+  each inside its own event pair; the median is reported beside the
+  back-to-back figure (`us_per_launch_flushed`).
 
 One JSON line goes to stdout:
 * value: algorithmic bytes of the K steps / wall time of the throughput pass
@@ -73,6 +78,7 @@ METRIC = "achieved HBM GB/s + % of peak: paged decode (B=64, ctx 4k) and add-RMS
 DECODE = {"batch": 64, "ctx": 4096, "num_q_heads": 32, "num_kv_heads": 8, "head_dim": 128, "page_size": 16}
 RMS = {"tokens": 4096, "hidden": 8192}
 COPY_BYTES = 1 << 30  # calibration copy: reads and writes this many bytes per dispatch
+FLUSH_BYTES = 1 << 30  # read before each launch of the flushed pass (> the 256 MB Infinity Cache)
 
 
 def log(msg: str) -> None:
@@ -361,6 +367,22 @@ def main(argv: list[str] | None = None) -> int:
     dom_ms = e0.elapsed_time(e1) / args.steps
     log(f"dominant-kernel pass: {args.steps} launches, {dom_ms * 1e3:.2f} us each")
     achieved = dom_work.bytes / (dom_ms * 1e-3) / 1e9
+
+    # Flushed pass: a 1 GiB read before every launch, an event pair around each.
+    flush = torch.ones(FLUSH_BYTES // 4, dtype=torch.float32, device=device)
+    flushed = []
+    for _ in range(args.steps):
+        flush.sum()
+        f0, f1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        f0.record(stream)
+        dom_op()
+        f1.record(stream)
+        f1.synchronize()
+        flushed.append(f0.elapsed_time(f1))
+    del flush
+    flushed.sort()
+    flushed_ms = flushed[len(flushed) // 2]
+    log(f"flushed dominant-kernel pass: {args.steps} launches, median {flushed_ms * 1e3:.2f} us")
     traffic, traffic_note = None, "not measured (--no-counters or a single-operator run)"
     if do_dec and not args.no_counters:
         traffic, traffic_note = measure_traffic()
@@ -372,6 +394,9 @@ def main(argv: list[str] | None = None) -> int:
         "unit": "GB/s",
         "frac": round(achieved / peak.dram_gbps, 4),
         "us_per_launch": round(dom_ms * 1e3, 2),
+        # A 1 GiB read before each launch, an event pair around it, median.
+        "us_per_launch_flushed": round(flushed_ms * 1e3, 2),
+        "frac_flushed": round(dom_work.bytes / (flushed_ms * 1e-3) / 1e9 / peak.dram_gbps, 4),
         "traffic": None if traffic is None else round(traffic),
         "traffic_over_algorithmic": None if traffic is None else round(traffic / dom_work.bytes, 4),
         "traffic_source": traffic_note,

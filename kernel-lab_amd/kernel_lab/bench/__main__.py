@@ -31,6 +31,12 @@ events on the launch stream around each call, median of --reps calls, with a
 read of a >= 512 MiB buffer before every call so inputs are not served from the
 256 MiB Infinity Cache (a read leaves clean lines, so no write-back lands in
 the timed call). GB/s uses the algorithmic byte model in roofline.py.
+
+A case's tensors go back to PyTorch's caching allocator, never to the driver
+(no empty_cache between cases): on MI355X, handing a 2 GiB block back to the
+driver slowed the next calls of an HBM-bound kernel by ~5 % (32/8/128 fp16
+B=64 ctx 4096 decode 158.8 -> 166.5 us) until about 2 s had passed, and made
+every case after the first look 5 % slower.
 """
 
 from __future__ import annotations
@@ -379,7 +385,6 @@ def decode_suite(
         atol = 2e-2 if dt != torch.float32 else 1e-3
         rows += measure("paged_decode", label, impls, work, peak, baseline, atol, timer)
         del q, kv, args, out, out2, impls
-        torch.cuda.empty_cache()
     return rows
 
 
@@ -431,7 +436,6 @@ def decode_fp8_suite(peak: GPUPeak | None, timer, shape: str | None = None) -> l
         # Scales rounded to the 16-bit type make the two caches differ by a rounding.
         rows += measure("paged_decode_fp8", label, impls, work, peak, baseline, 3e-2, timer)
         del q, kv, kv8, a16, a8, out16, out8, impls
-        torch.cuda.empty_cache()
     return rows
 
 
@@ -477,7 +481,6 @@ def cascade_suite(peak: GPUPeak | None, timer, shape: str | None = None) -> list
         work = {"hip paged decode (planner)": plain, "hip cascade": casc}
         rows += measure("cascade_decode", label, impls, work, peak, "hip paged decode (planner)", 3e-2, timer)
         del q, c, flat, o_plain, o_casc, impls
-        torch.cuda.empty_cache()
     return rows
 
 
@@ -494,7 +497,6 @@ def copy_suite(peak: GPUPeak | None, timer, mib: int = 1024) -> list[Row]:
     work = Work(bytes=2 * n * 4, flops=0)
     rows = measure("copy", f"{mib} MiB", {"torch copy_": lambda: y.copy_(x)}, work, peak, "torch copy_", 0.0, timer)
     del x, y
-    torch.cuda.empty_cache()
     return rows
 
 
@@ -573,7 +575,6 @@ def configs_suite(peak: GPUPeak | None, timer, shape: str | None = None) -> tupl
         order.append({"cfg": cfg, "case": label, "calls": 1 + WARMUP_CALLS + timer.reps, "timed": timer.reps,
                       "bytes": work.bytes})
         del expected, out
-        torch.cuda.empty_cache()
     return rows, order
 
 
