@@ -262,8 +262,9 @@ def torch_sdpa_decode(q, k_cache, v_cache, block_table, seq_lens, scale, padded:
     there): pages gathered into padded K/V, then scaled_dot_product_attention.
 
     Only SDPA's fused kernels may serve the call: its math fallback runs
-    batched 16-bit products on a transposed view of K, a form that has faulted
-    the GPU on this platform. On this build's SDPA (probed on MI355X, fp16 and
+    batched 16-bit products (torch.bmm) whose right operand is a transposed
+    view of K, a form reported to fault GPUs on the MI355X pool this was built
+    on, so it is never run. On this build's SDPA (probed on MI355X, fp16 and
     bf16), the flash kernel takes grouped-query heads only without a mask,
     and the memory-efficient kernel takes a mask only with K/V expanded to
     every query head. So a batch whose sequences all fill the block table
