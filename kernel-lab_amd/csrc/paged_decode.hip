@@ -70,6 +70,10 @@ constexpr int kMaxPlannedSplits = 64;
 constexpr int kMinPagesPerSplit = 16;      // fewest pages a planned uniform split takes
 constexpr int kMinPagesPerSingleSplit = 8;  // the same for a batch of one sequence
 constexpr int kMinPagesPerBalancedWg = 8;  // fewest pages a balanced-schedule workgroup takes
+// The balanced cut's charge for a segment start, in K/V bytes of one
+// workgroup's stream (balanced_charge), and its cap in pages.
+constexpr int64_t kSegmentStartBytes = 128 * 1024;
+constexpr int kMaxSegmentCharge = 64;
 constexpr int kFusedMaxSegments = 8;       // most segments of a balanced unit merged in the kernel
 constexpr int kMinSegmentPages = 32;       // ... while its segments are shorter than this (make_plan)
 // Cache policy of the K/V loads: streamed once, so non-temporal. Measured on
@@ -131,6 +135,10 @@ struct DecodeArgs {
   // batch has at most 64 * kScanChunks sequences, else 0 (see
   // decode_mfma_balanced_kernel's even-batch start).
   int even_start;
+  // Balanced kernel: list positions the cut charges for starting a unit's
+  // segment, on top of its pages (balanced_charge); the kernel applies it to
+  // uneven batches of at most 64 * kScanChunks sequences only.
+  int seg_charge;
   float scale_log2;     // scale * log2(e)
   // Query-row mapping. Local head hl of KV head kvh in sequence b reads q row
   // (b + hl / q_fold) * q_heads + kvh * q_fold + hl % q_fold, and the output
@@ -360,7 +368,7 @@ __device__ __forceinline__ void fetch_args(const DecodeArgs& a) {
   asm volatile("" ::"s"(a.token_stride), "s"(a.batch), "s"(a.num_q_heads), "s"(a.num_kv_heads), "s"(a.group),
                "s"(a.page_size), "s"(a.bpp_magic), "s"(a.bpp_shift), "s"(a.max_pages), "s"(a.num_splits),
                "s"(a.pages_per_split), "s"(a.head_groups), "s"(a.heads_per_wg), "s"(a.grid), "s"(a.even_start),
-               "s"(a.scale_log2),
+               "s"(a.seg_charge), "s"(a.scale_log2),
                "s"(a.q_fold), "s"(a.q_heads), "s"(a.force_partial));
 }
 
@@ -1196,32 +1204,50 @@ __device__ __forceinline__ int64_t list_total(const DecodeArgs& a, int units_per
   return total;
 }
 
-// Length of the work list, the list position where sequence b's units begin
-// and sequence b's page count (b wave-uniform).
-__device__ __forceinline__ void list_prefix(const DecodeArgs& a, int units_per_seq, int b, int64_t* total,
-                                            int64_t* base, int* pages) {
-  const int lane = __lane_id();
-  int64_t t = 0, pre = 0;
-  int own = 0;
-  for (int b0 = 0; b0 < a.batch; b0 += 64) {
-    const int bb = b0 + lane;
-    const int np = bb < a.batch ? seq_pages(a, bb) : 0;
-    const int pl = np * units_per_seq;
-    const int incl = wave_incl_scan(pl);
-    if (b >= b0 && b < b0 + 64) {
-      pre = t + __builtin_amdgcn_readlane(incl - pl, b - b0);
-      own = __builtin_amdgcn_readlane(np, b - b0);
-    }
-    t += __builtin_amdgcn_readlane(incl, 63);
-  }
-  *total = t;
-  *base = pre;
-  *pages = own;
-}
-
 // Batches of up to 64 * kScanChunks sequences are scanned with all their
 // seq_lens loads in flight at once: one memory round trip at the start.
 constexpr int kScanChunks = 4;
+
+// The balanced work list. Each pages-bearing sequence contributes
+// units_per_seq units in order; a unit takes charge + n list positions, the
+// charge first (no pages: the cut's cost of starting a segment there) and
+// then its n pages. charge is a.seg_charge for a batch of at most 64 *
+// kScanChunks sequences whose page counts are not all equal, else 0 (an
+// even batch's units are cut at their own boundaries already, and a charge
+// would only take pages from the workgroups that start a unit). Workgroup w
+// takes list positions [w * per, (w + 1) * per).
+//
+// Length of the work list, the list position where sequence b's units begin,
+// sequence b's page count and the charge (b wave-uniform), as the balanced
+// kernel's schedule_start computes them.
+__device__ __forceinline__ void list_prefix(const DecodeArgs& a, int units_per_seq, int b, int64_t* total,
+                                            int64_t* base, int* pages, int* charge) {
+  const int lane = __lane_id();
+  int64_t t = 0, pre = 0;
+  int own = 0, seqs = 0, seqs_before = 0;
+  const int n0 = seq_pages(a, 0);
+  bool differ = n0 == 0;
+  for (int b0 = 0; b0 < a.batch; b0 += 64) {
+    const int bb = b0 + lane;
+    const int np = bb < a.batch ? seq_pages(a, bb) : 0;
+    differ |= bb < a.batch && np != n0;
+    const int pl = np * units_per_seq;
+    const int incl = wave_incl_scan(pl);
+    const uint64_t bearing = __ballot(np > 0);
+    if (b >= b0 && b < b0 + 64) {
+      pre = t + __builtin_amdgcn_readlane(incl - pl, b - b0);
+      own = __builtin_amdgcn_readlane(np, b - b0);
+      seqs_before = seqs + __builtin_popcountll(bearing & ((1ull << (b - b0)) - 1));
+    }
+    t += __builtin_amdgcn_readlane(incl, 63);
+    seqs += __builtin_popcountll(bearing);
+  }
+  const int c = a.batch <= 64 * kScanChunks && __ballot(differ) != 0 ? a.seg_charge : 0;
+  *total = t + static_cast<int64_t>(c) * units_per_seq * seqs;
+  *base = pre + static_cast<int64_t>(c) * units_per_seq * seqs_before;
+  *pages = own;
+  *charge = c;
+}
 
 // Where workgroup `wg` starts: its first list position `pos` (wg * per), the
 // first pages-bearing sequence whose units hold it (batch when pos is past the
@@ -1230,8 +1256,9 @@ constexpr int kScanChunks = 4;
 struct Start {
   int64_t total, per, pos, base;
   int b;
-  int pages;  // pages of sequence b (when b < batch)
-  int len;    // its length, clamped to max_pages * page_size
+  int pages;   // pages of sequence b (when b < batch)
+  int len;     // its length, clamped to max_pages * page_size
+  int charge;  // list positions ahead of each unit's pages (list_prefix)
   // batch <= 64 * kScanChunks only: bit j of empties[k] marks sequence
   // 64 * k + j as existing, without pages, and zeroed by this workgroup
   // (sequence b belongs to workgroup b % grid: the grid may be smaller than
@@ -1312,7 +1339,9 @@ __device__ __forceinline__ Start schedule_start(const DecodeArgs& a, int units_p
   for (int k = 0; k < kScanChunks; ++k) s.empties[k] = 0;
   s.pages = 0;
   s.len = 0;
+  s.charge = 0;
   if (a.batch <= 64 * kScanChunks) {
+    s.charge = even_pages(a, c) > 0 ? 0 : a.seg_charge;
     int len[kScanChunks], pl[kScanChunks], incl[kScanChunks];
     int64_t before[kScanChunks];
 #pragma unroll
@@ -1324,7 +1353,8 @@ __device__ __forceinline__ Start schedule_start(const DecodeArgs& a, int units_p
       incl[k] = 0;
       before[k] = total;
       if (64 * k < a.batch) {
-        pl[k] = pages_of(a, len[k]) * units_per_seq;
+        const int np = pages_of(a, len[k]);
+        pl[k] = np > 0 ? (np + s.charge) * units_per_seq : 0;
         incl[k] = wave_incl_scan(pl[k]);
         total += __builtin_amdgcn_readlane(incl[k], 63);
         const int b = 64 * k + lane;
@@ -1343,7 +1373,7 @@ __device__ __forceinline__ Start schedule_start(const DecodeArgs& a, int units_p
         const int j = __builtin_ctzll(__ballot(before[k] + incl[k] > s.pos));
         s.b = 64 * k + j;
         s.base = before[k] + __builtin_amdgcn_readlane(incl[k] - pl[k], j);
-        s.pages = __builtin_amdgcn_readlane(pl[k], j) / units_per_seq;
+        s.pages = __builtin_amdgcn_readlane(pl[k], j) / units_per_seq - s.charge;
         s.len = __builtin_amdgcn_readlane(len[k], j);
         found = true;
       }
@@ -1374,6 +1404,7 @@ __device__ __forceinline__ Start schedule_start(const DecodeArgs& a, int units_p
   s.b = __builtin_amdgcn_readfirstlane(s.b);
   s.pages = __builtin_amdgcn_readfirstlane(s.pages);
   s.len = __builtin_amdgcn_readfirstlane(s.len);
+  s.charge = __builtin_amdgcn_readfirstlane(s.charge);
   return s;
 }
 
@@ -1499,68 +1530,77 @@ __global__ void __launch_bounds__(PAIR * kThreads, (mfma_waves_per_eu<D, NT>()))
   int64_t base = st.base;
   int n = st.pages;   // pages of sequence b
   int len = st.len;   // its clamped length
+  const int charge = st.charge;
 
   while (pos < end && b < a.batch) {
     // b is pages-bearing: the start and the advance below skip empty sequences.
-    // The offset inside sequence b's units is below hp * max_pages, so 32-bit
-    // arithmetic splits it into a unit and a page (a 64-bit division here,
-    // scalar and in software, cost ~0.5 us before every segment's first load).
+    // The offset inside sequence b's units is below hp * (max_pages + charge),
+    // so 32-bit arithmetic splits it into a unit and a position (a 64-bit
+    // division here, scalar and in software, cost ~0.5 us before every
+    // segment's first load). A unit spans charge + n list positions, its
+    // pages after the charge (list_prefix).
+    const int span = n + charge;
     const uint32_t off = static_cast<uint32_t>(pos - base);
-    const uint32_t ru = off / static_cast<uint32_t>(n);
+    const uint32_t ru = off / static_cast<uint32_t>(span);
     const int r = static_cast<int>(ru);
-    const int page0 = static_cast<int>(off - ru * static_cast<uint32_t>(n));
-    const int64_t unit_base = base + static_cast<int64_t>(r) * n;
-    const int page1 = static_cast<int>(min(static_cast<int64_t>(n), end - unit_base));
+    const int at = static_cast<int>(off - ru * static_cast<uint32_t>(span));
+    const int64_t unit_base = base + static_cast<int64_t>(r) * span;
+    const int64_t page_base = unit_base + charge;  // list position of the unit's page 0
+    const int page0 = max(0, at - charge);
+    // At most page0 only when the range ends inside the unit's charge: no pages here.
+    const int page1 = static_cast<int>(min(static_cast<int64_t>(n), end - page_base));
+    if (page1 > page0) {
+      // The unit is wave-uniform, but the compiler cannot prove it through the
+      // scan above; without readfirstlane the buffer descriptors built from it
+      // land in VGPRs and every K/V load becomes a per-lane waterfall loop.
+      Unit u;
+      u.b = __builtin_amdgcn_readfirstlane(b);
+      const int rkv = a.head_groups == 1 ? r : r / a.head_groups;  // one head group is the common case
+      u.kvh = __builtin_amdgcn_readfirstlane(rkv * PAIR + half);
+      u.hg = __builtin_amdgcn_readfirstlane(r - rkv * a.head_groups);
+      u.split = 0;
+      u.seq_len = __builtin_amdgcn_readfirstlane(len);
+      u.page_begin = __builtin_amdgcn_readfirstlane(page0);
+      u.page_end = __builtin_amdgcn_readfirstlane(page1);
 
-    // The unit is wave-uniform, but the compiler cannot prove it through the
-    // scan above; without readfirstlane the buffer descriptors built from it
-    // land in VGPRs and every K/V load becomes a per-lane waterfall loop.
-    Unit u;
-    u.b = __builtin_amdgcn_readfirstlane(b);
-    const int rkv = a.head_groups == 1 ? r : r / a.head_groups;  // one head group is the common case
-    u.kvh = __builtin_amdgcn_readfirstlane(rkv * PAIR + half);
-    u.hg = __builtin_amdgcn_readfirstlane(r - rkv * a.head_groups);
-    u.split = 0;
-    u.seq_len = __builtin_amdgcn_readfirstlane(len);
-    u.page_begin = __builtin_amdgcn_readfirstlane(page0);
-    u.page_end = __builtin_amdgcn_readfirstlane(page1);
+      const int64_t slot = (static_cast<int64_t>(w) + static_cast<int64_t>(b) * hp + r) * PAIR + half;
+      Dest dst;
+      dst.final = page0 == 0 && page1 == n;
+      dst.o = a.o_part + slot * a.heads_per_wg * D;
+      dst.lse = a.lse_part + slot * a.heads_per_wg;
+      dst.o_head_stride = D;
+      dst.lse_head_stride = 1;
 
-    const int64_t slot = (static_cast<int64_t>(w) + static_cast<int64_t>(b) * hp + r) * PAIR + half;
-    Dest dst;
-    dst.final = page0 == 0 && page1 == n;
-    dst.o = a.o_part + slot * a.heads_per_wg * D;
-    dst.lse = a.lse_part + slot * a.heads_per_wg;
-    dst.o_head_stride = D;
-    dst.lse_head_stride = 1;
-
-    // The previous segment's waves may still read LDS; before the first
-    // segment nothing has used it (the schedule needs no LDS), so no barrier.
-    if (pos != st.pos) __syncthreads();
-    mfma_segment<E, KVF, D, NT, W>(a, lds + half * Lds::kBytes, u, dst, hw);
-    if (NT == 1 && !dst.final && a.arrivals != nullptr) {  // see kFusedMergeMaxHeads
-      // The unit's segments are workgroups w0 .. w1 (slots (w + list unit) * PAIR + half).
-      const int64_t w0 = unit_base / st.per;
-      const int64_t w1 = (unit_base + n - 1) / st.per;
-      const int64_t slot0 = (w0 + static_cast<int64_t>(b) * hp + r) * PAIR + half;
-      const int h0 = u.hg * a.heads_per_wg;
-      MergeJob job;
-      job.lse = a.lse_part + slot0 * a.heads_per_wg;
-      job.lse_head_stride = 1;
-      job.l_stride = static_cast<int64_t>(PAIR) * a.heads_per_wg;
-      job.o = a.o_part + slot0 * a.heads_per_wg * D;
-      job.o_head_stride = D;
-      job.o_stride = static_cast<int64_t>(PAIR) * a.heads_per_wg * D;
-      job.n = static_cast<int>(w1 - w0) + 1;
-      job.heads = min(a.heads_per_wg, a.group - h0);
-      job.out = static_cast<typename E::S*>(a.out) +
-                (static_cast<int64_t>(u.b) * a.num_q_heads + u.kvh * a.group + h0) * D;
-      const int64_t unit = (static_cast<int64_t>(u.b) * a.num_kv_heads + u.kvh) * a.head_groups + u.hg;
-      arrive_and_merge<E, W>(a.arrivals + unit, job, D, hw, s_last + half);
+      // The previous segment's waves may still read LDS; before the first
+      // segment nothing has used it (the schedule needs no LDS), so no barrier.
+      if (pos != st.pos) __syncthreads();
+      mfma_segment<E, KVF, D, NT, W>(a, lds + half * Lds::kBytes, u, dst, hw);
+      if (NT == 1 && !dst.final && a.arrivals != nullptr) {  // see kFusedMergeMaxHeads
+        // The unit's segments are workgroups w0 .. w1, those whose ranges hold
+        // its first and last page (slots (w + list unit) * PAIR + half).
+        const int64_t w0 = page_base / st.per;
+        const int64_t w1 = (page_base + n - 1) / st.per;
+        const int64_t slot0 = (w0 + static_cast<int64_t>(b) * hp + r) * PAIR + half;
+        const int h0 = u.hg * a.heads_per_wg;
+        MergeJob job;
+        job.lse = a.lse_part + slot0 * a.heads_per_wg;
+        job.lse_head_stride = 1;
+        job.l_stride = static_cast<int64_t>(PAIR) * a.heads_per_wg;
+        job.o = a.o_part + slot0 * a.heads_per_wg * D;
+        job.o_head_stride = D;
+        job.o_stride = static_cast<int64_t>(PAIR) * a.heads_per_wg * D;
+        job.n = static_cast<int>(w1 - w0) + 1;
+        job.heads = min(a.heads_per_wg, a.group - h0);
+        job.out = static_cast<typename E::S*>(a.out) +
+                  (static_cast<int64_t>(u.b) * a.num_q_heads + u.kvh * a.group + h0) * D;
+        const int64_t unit = (static_cast<int64_t>(u.b) * a.num_kv_heads + u.kvh) * a.head_groups + u.hg;
+        arrive_and_merge<E, W>(a.arrivals + unit, job, D, hw, s_last + half);
+      }
     }
 
-    pos = unit_base + page1;
+    pos = page_base + page1;  // end, or the next unit's first list position
     if (pos < end && r == hp - 1 && page1 == n) {  // more to do past this sequence: next non-empty one
-      base += static_cast<int64_t>(n) * hp;
+      base += static_cast<int64_t>(span) * hp;
       do {
         b = __builtin_amdgcn_readfirstlane(b + 1);
         len = b < a.batch ? clamped_len(a, as_constant(a.seq_lens)[b]) : 0;
@@ -1939,8 +1979,8 @@ __global__ void __launch_bounds__(64) decode_merge_balanced_kernel(const DecodeA
   const int pair = a.paired ? 2 : 1;  // list units are KV-head pairs (decode_mfma_balanced_kernel<..., 2>)
   const int hp = a.num_kv_heads * a.head_groups / pair;
   int64_t total, base;  // list length; list position of sequence b's first unit
-  int n;                // sequence b's pages
-  list_prefix(a, hp, b, &total, &base, &n);
+  int n, charge;        // sequence b's pages; list positions ahead of each unit's pages
+  list_prefix(a, hp, b, &total, &base, &n, &charge);
   S* out = static_cast<S*>(a.out) + (static_cast<int64_t>(b) * a.num_q_heads + head) * head_dim;
   if (n == 0) {
     // No cached token: the softmax-weighted sum over no values is zero.
@@ -1949,9 +1989,9 @@ __global__ void __launch_bounds__(64) decode_merge_balanced_kernel(const DecodeA
   }
   const int64_t per = balanced_per(a, total);
   const int r = (kvh / pair) * a.head_groups + hg;
-  const int64_t unit_base = base + static_cast<int64_t>(r) * n;
-  const int64_t w0 = unit_base / per;
-  const int64_t w1 = (unit_base + n - 1) / per;
+  const int64_t page_base = base + static_cast<int64_t>(r) * (n + charge) + charge;  // the unit's page 0
+  const int64_t w0 = page_base / per;
+  const int64_t w1 = (page_base + n - 1) / per;
   if (w0 == w1) return;
   const int64_t uidx = static_cast<int64_t>(b) * hp + r;
   const int64_t slot0 = (w0 + uidx) * pair + kvh % pair;  // consecutive workgroups' slots are `pair` apart
@@ -2579,6 +2619,15 @@ int launch_uniform_mfma(const DecodeArgs& a, int head_dim, unsigned grid, hipStr
   });
 }
 
+// The balanced cut's charge for starting a segment (list_prefix), in pages of
+// one list unit: the bytes a workgroup streams in about the time a segment's
+// start and end take (first K/V round trip after the schedule, cross-wave
+// merge, partial store), kSegmentStartBytes, over one page's K and V bytes.
+int balanced_charge(int page_size, int head_dim, int kv_bytes, int paired) {
+  const int64_t page_bytes = static_cast<int64_t>(page_size) * head_dim * kv_bytes * 2 * (paired ? 2 : 1);
+  return static_cast<int>(std::min<int64_t>(kMaxSegmentCharge, cdiv(kSegmentStartBytes, page_bytes)));
+}
+
 template <typename E, typename KVF>
 int launch_balanced(DecodeArgs a, int head_dim, hipStream_t stream) {
   const unsigned grid = static_cast<unsigned>(a.grid);
@@ -2587,6 +2636,7 @@ int launch_balanced(DecodeArgs a, int head_dim, hipStream_t stream) {
   // seq_lens in one wave-wide scan.
   const int64_t lunits = a.paired ? units / 2 : units;
   a.even_start = a.grid == lunits && a.batch <= 64 * kScanChunks ? 1 : 0;
+  a.seg_charge = balanced_charge(a.page_size, head_dim, KVF::kBytes, a.paired);
   a.arrivals = fused_merge_counters(a, units, stream);
   int st = dispatch_mfma(head_dim, a.heads_per_wg, [&](auto d, auto nt) -> int {
     constexpr int D = decltype(d)::value, NT = decltype(nt)::value;
@@ -2741,6 +2791,7 @@ int decode_entry(kl_dtype dtype, bool kv8, void* out, const void* q, const void*
   a.head_groups = p.head_groups;
   a.grid = p.grid;
   a.even_start = 0;  // set by launch_balanced
+  a.seg_charge = 0;
   a.heads_per_wg = p.heads_per_wg;
   a.scale_log2 = scale * kLog2e;
   a.q_fold = a.group;

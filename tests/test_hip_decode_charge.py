@@ -1,0 +1,96 @@
+"""The balanced cut's segment charge.
+
+On a batch of at most 256 sequences whose page counts differ, the balanced
+schedule's work list gives every unit a few list positions ahead of its
+pages (the charge, about what starting a segment costs), so a workgroup
+whose range starts a unit takes fewer pages; an even batch (one page count)
+and a batch of more than 256 sequences are cut without it. The cases below
+reach the cut's edges: ranges that end inside a charge (a batch of one-page
+sequences beside a long one, so a workgroup's range is shorter than a
+charge), a batch that differs by one page, lengths that differ but not in
+pages (no charge), empty sequences, MQA units (merge kernel), paired KV
+heads, head_dim 64, the FP8 cache and a batch past the scan's 256
+sequences. A page the cut dropped or took twice changes the output, so
+each case checks the oracle on up to 8 sequences (the longest among them),
+through the planner and on the balanced schedule, and there the merge kernel
+against the in-kernel merge, whose unit ranges are computed by different
+code (the merge kernel's list_prefix, the decode kernel's schedule_start),
+bit for bit.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from kernel_lab import _native
+from kernel_lab.kv_cache import quantize_fp8, random_decode_problem
+from oracle import reference as ref
+from tests.conftest import decode_parity
+
+pytestmark = pytest.mark.gpu
+
+
+def _lens(spec) -> list[int]:
+    if isinstance(spec, str):  # "u<max>x<batch>": uniform in [1, max]
+        hi, batch = (int(v) for v in spec[1:].split("x"))
+        g = torch.Generator().manual_seed(hi + batch)
+        return torch.randint(1, hi + 1, (batch,), generator=g).tolist()
+    return list(spec)
+
+
+CASES = [
+    # (lens, hq, hkv, head_dim, dtype, fp8, empty sequences)
+    ([1] * 63 + [5000], 32, 8, 128, torch.float16, False, []),  # ranges shorter than a charge
+    ([2048] * 31 + [2032], 32, 8, 128, torch.float16, False, []),  # one page short: charged
+    ([2048] * 31 + [2047], 32, 8, 128, torch.float16, False, []),  # same page counts: even
+    ("u2000x32", 32, 8, 128, torch.float16, False, [4, 17]),
+    ("u2500x64", 32, 8, 128, torch.bfloat16, False, []),  # paired KV heads
+    ("u300x48", 32, 1, 128, torch.bfloat16, False, [0]),  # MQA: merge kernel
+    ("u8192x16", 32, 1, 128, torch.bfloat16, False, []),
+    ("u3000x64", 16, 2, 64, torch.bfloat16, False, [63]),  # head_dim 64
+    ("u1500x40", 32, 8, 128, torch.float16, True, [7]),  # FP8 cache
+    ("u600x200", 32, 8, 128, torch.float16, False, []),
+    ("u600x300", 32, 8, 128, torch.float16, False, [299]),  # past the scan: no charge
+]
+
+
+@pytest.mark.parametrize(("spec", "hq", "hkv", "head_dim", "dtype", "fp8", "empty"), CASES)
+@pytest.mark.parametrize("schedule", ["planner", "balanced"])
+def test_charged_cut(gpu_ops, spec, hq, hkv, head_dim, dtype, fp8, empty, schedule):
+    lens = _lens(spec)
+    q, kv, _, _ = random_decode_problem(lens, hq, hkv, head_dim, 16, dtype=dtype, device="cuda",
+                                        poison=float("nan"))
+    kv.seq_lens[empty] = 0
+    kw = {} if schedule == "planner" else {"num_splits": gpu_ops.BALANCED}
+    if fp8:
+        kv8, ks, vs = quantize_fp8(kv)
+        run = lambda: gpu_ops.paged_decode_attention(q, kv8.k_cache, kv8.v_cache, kv.block_table, kv.seq_lens,
+                                                     k_scale=ks, v_scale=vs, **kw)
+    else:
+        run = lambda: gpu_ops.paged_decode_attention(q, kv.k_cache, kv.v_cache, kv.block_table, kv.seq_lens, **kw)
+    got = run().cpu()
+    assert torch.isfinite(got).all(), "non-finite output: a poisoned page or tail leaked in"
+    if schedule == "balanced":
+        # (The planner's own choice of schedule depends on whether the
+        # in-kernel merge is available, so it is compared on the balanced
+        # schedule only.)
+        with _native.decode_switches(fused_merge="0"):
+            merged = run().cpu()
+        assert torch.equal(got, merged), "the in-kernel merge and the merge kernel disagree on the cut"
+    for b in empty:
+        assert not got[b].any(), "an empty sequence must give zeros"
+    live = [b for b in range(len(lens)) if b not in empty]
+    longest = max(live, key=lambda b: lens[b])
+    rows = sorted({longest, *live[:4], *live[-3:]})
+    if fp8:
+        want = ref.paged_decode_attention_fp8(
+            q[rows].cpu().float(), kv8.k_cache.cpu(), kv8.v_cache.cpu(), kv.block_table[rows].cpu(),
+            kv.seq_lens[rows].cpu(), ks.cpu(), vs.cpu()
+        )
+    else:
+        want = ref.paged_decode_attention(
+            q[rows].cpu().float(), kv.k_cache.cpu(), kv.v_cache.cpu(), kv.block_table[rows].cpu(),
+            kv.seq_lens[rows].cpu()
+        )
+    decode_parity(got[rows], want, dtype)
