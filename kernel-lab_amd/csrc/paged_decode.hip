@@ -2398,7 +2398,14 @@ int make_plan(const Options& opt, kl_dtype dtype, int batch, int num_q_heads, in
   const int full_batch_choice = opt.balance();  // 1 balanced, 0 uniform, -1 by default
   const bool full_default =
       (p->heads_per_wg <= kFusedMergeMaxHeads && opt.fused_merge()) || pages >= kBalanceMinPages;
-  const bool requested = num_splits == KL_SPLITS_BALANCED;
+  // The balanced kernel sums 64 sequences' list lengths (their units' pages
+  // and charges) in 32-bit lanes and splits a position inside one sequence's
+  // units with a 32-bit division; tables long enough to pass 2^31 there keep
+  // uniform splits, requested or not.
+  const bool list_fits = static_cast<int64_t>(64) * num_kv_heads * p->head_groups *
+                             (static_cast<int64_t>(pages) + kMaxSegmentCharge) <= 0x7fffffffLL;
+  const bool requested = num_splits == KL_SPLITS_BALANCED && list_fits;
+  if (num_splits == KL_SPLITS_BALANCED && !list_fits) num_splits = 0;
   // One sequence cannot be skewed: uniform splits cut it as evenly as the
   // balanced schedule would, without its start (the seq_lens scan before the
   // first block-table load) or its merge's search for each unit's slots.
@@ -2407,7 +2414,7 @@ int make_plan(const Options& opt, kl_dtype dtype, int batch, int num_q_heads, in
   // 8/1/128 ctx 32768 26.08 -> 16.40.
   const bool single = batch == 1 && !long_pairs;
   const bool automatic =
-      num_splits == 0 && !single &&
+      num_splits == 0 && !single && list_fits &&
       (units < cus || (full_batch_choice < 0 ? full_default : full_batch_choice == 1));
   const bool balance = requested || automatic;
   const bool pair_balanced = pairable && balance;

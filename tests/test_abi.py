@@ -217,6 +217,20 @@ def test_requested_balanced_schedule_at_any_batch():
         ops.plan_decode(torch.float16, 2, 4, 2, 32, 16, 4, -2)
 
 
+@pytest.mark.parametrize(("max_pages", "balanced"), [(4194239, True), (4194240, False)])
+def test_balanced_schedule_needs_list_lengths_in_32_bits(max_pages, balanced):
+    """The balanced kernel sums 64 sequences' list lengths (each unit's pages
+    plus a charge of at most 64 positions) in 32-bit lanes: 64 x 8 units x
+    (max_pages + 64) must stay below 2^31, or the planner keeps uniform
+    splits, also when the balanced schedule is requested."""
+    for requested in (0, ops.BALANCED):
+        splits, ws = ops.plan_decode(torch.float16, 64, 32, 8, 128, 16, max_pages, requested, 256)
+        if balanced:
+            assert splits == 0 and ws > 0
+        else:
+            assert splits >= 1
+
+
 @pytest.mark.parametrize(("requested", "max_pages", "want"), [(1, 5, 1), (2, 5, 2), (3, 5, 3), (5, 5, 5), (64, 5, 5), (4, 7, 4), (5, 7, 4)])
 def test_requested_splits_normalise_like_the_original(requested, max_pages, want):
     """pages_per_split = cdiv(max_pages, S); S = cdiv(max_pages, pages_per_split)
