@@ -2629,10 +2629,14 @@ int launch_uniform_mfma(const DecodeArgs& a, int head_dim, unsigned grid, hipStr
 // The balanced cut's charge for starting a segment (list_prefix), in pages of
 // one list unit: the bytes a workgroup streams in about the time a segment's
 // start and end take (first K/V round trip after the schedule, cross-wave
-// merge, partial store), kSegmentStartBytes, over one page's K and V bytes.
-int balanced_charge(int page_size, int head_dim, int kv_bytes, int paired) {
-  const int64_t page_bytes = static_cast<int64_t>(page_size) * head_dim * kv_bytes * 2 * (paired ? 2 : 1);
-  return static_cast<int>(std::min<int64_t>(kMaxSegmentCharge, cdiv(kSegmentStartBytes, page_bytes)));
+// merge: kSegmentStartBytes) plus the partial it adds (its fp32 rows, written
+// by the segment and read back by the merge), over one page's K and V bytes.
+int balanced_charge(int page_size, int head_dim, int kv_bytes, int paired, int heads_per_wg) {
+  const int halves = paired ? 2 : 1;
+  const int64_t page_bytes = static_cast<int64_t>(page_size) * head_dim * kv_bytes * 2 * halves;
+  const int64_t partial_bytes = static_cast<int64_t>(heads_per_wg) * head_dim * 4 * halves;
+  return static_cast<int>(
+      std::min<int64_t>(kMaxSegmentCharge, cdiv(kSegmentStartBytes + 2 * partial_bytes, page_bytes)));
 }
 
 template <typename E, typename KVF>
@@ -2643,7 +2647,7 @@ int launch_balanced(DecodeArgs a, int head_dim, hipStream_t stream) {
   // seq_lens in one wave-wide scan.
   const int64_t lunits = a.paired ? units / 2 : units;
   a.even_start = a.grid == lunits && a.batch <= 64 * kScanChunks ? 1 : 0;
-  a.seg_charge = balanced_charge(a.page_size, head_dim, KVF::kBytes, a.paired);
+  a.seg_charge = balanced_charge(a.page_size, head_dim, KVF::kBytes, a.paired, a.heads_per_wg);
   a.arrivals = fused_merge_counters(a, units, stream);
   int st = dispatch_mfma(head_dim, a.heads_per_wg, [&](auto d, auto nt) -> int {
     constexpr int D = decltype(d)::value, NT = decltype(nt)::value;
