@@ -130,7 +130,11 @@ int kl_paged_decode_plan(kl_dtype dtype, int batch, int num_q_heads, int num_kv_
  * num_kv_heads (grouped-query attention). `scale` multiplies q.k.
  * num_splits == 0 lets the planner choose; KL_SPLITS_BALANCED (-1) cuts the
  * pages of all sequences into equal per-workgroup ranges on the device, which
- * suits batches of very uneven lengths. The workspace must hold at least
+ * suits batches of very uneven lengths (on a batch of at most 256 sequences
+ * whose page counts differ, each (sequence, KV head) unit also counts a few
+ * pages for the segment start it costs, so ranges that start a unit are
+ * shorter). Block tables long enough that 64 sequences' units would pass
+ * 2^31 pages take uniform splits instead. The workspace must hold at least
  * the bytes kl_paged_decode_plan reports for the same arguments; it may be
  * NULL when that is 0. batch == 0 is a successful no-op.
  *
