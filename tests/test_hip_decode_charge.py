@@ -9,8 +9,8 @@ reach the cut's edges: ranges that end inside a charge (a batch of one-page
 sequences beside a long one, so a workgroup's range is shorter than a
 charge), a batch that differs by one page, lengths that differ but not in
 pages (no charge), empty sequences, MQA units (merge kernel), paired KV
-heads, head_dim 64, the FP8 cache and a batch past the scan's 256
-sequences. A page the cut dropped or took twice changes the output, so
+heads, head_dim 32, 64 and 256, pages of 32 and 64 tokens, the FP8 cache
+and a batch past the scan's 256 sequences. A page the cut dropped or took twice changes the output, so
 each case checks the oracle on up to 8 sequences (the longest among them),
 through the planner and on the balanced schedule, and there the merge kernel
 against the in-kernel merge, whose unit ranges are computed by different
@@ -40,7 +40,7 @@ def _lens(spec) -> list[int]:
 
 
 CASES = [
-    # (lens, hq, hkv, head_dim, dtype, fp8, empty sequences)
+    # (lens, hq, hkv, head_dim, dtype, fp8, empty sequences[, page_size])
     ([1] * 63 + [5000], 32, 8, 128, torch.float16, False, []),  # ranges shorter than a charge
     ([2048] * 31 + [2032], 32, 8, 128, torch.float16, False, []),  # one page short: charged
     ([2048] * 31 + [2047], 32, 8, 128, torch.float16, False, []),  # same page counts: even
@@ -52,14 +52,19 @@ CASES = [
     ("u1500x40", 32, 8, 128, torch.float16, True, [7]),  # FP8 cache
     ("u600x200", 32, 8, 128, torch.float16, False, []),
     ("u600x300", 32, 8, 128, torch.float16, False, [299]),  # past the scan: no charge
+    ("u5000x24", 32, 8, 128, torch.bfloat16, False, [5], 64),  # 64-token pages: 4 blocks per page
+    ("u4000x16", 16, 4, 256, torch.float16, False, [], 32),  # head_dim 256, 32-token pages
+    ("u3000x40", 8, 2, 32, torch.bfloat16, False, [1]),  # head_dim 32: the charge at its cap
 ]
 
 
-@pytest.mark.parametrize(("spec", "hq", "hkv", "head_dim", "dtype", "fp8", "empty"), CASES)
+@pytest.mark.parametrize("case", CASES)
 @pytest.mark.parametrize("schedule", ["planner", "balanced"])
-def test_charged_cut(gpu_ops, spec, hq, hkv, head_dim, dtype, fp8, empty, schedule):
+def test_charged_cut(gpu_ops, case, schedule):
+    spec, hq, hkv, head_dim, dtype, fp8, empty = case[:7]
+    page_size = case[7] if len(case) > 7 else 16
     lens = _lens(spec)
-    q, kv, _, _ = random_decode_problem(lens, hq, hkv, head_dim, 16, dtype=dtype, device="cuda",
+    q, kv, _, _ = random_decode_problem(lens, hq, hkv, head_dim, page_size, dtype=dtype, device="cuda",
                                         poison=float("nan"))
     kv.seq_lens[empty] = 0
     kw = {} if schedule == "planner" else {"num_splits": gpu_ops.BALANCED}
