@@ -176,7 +176,10 @@ int kl_paged_decode_last_merge(void);
  *   KL_DECODE_PAIRED=0            no two-KV-head workgroups
  *   KL_DECODE_BALANCE_ALWAYS=1|0  full batches always / never balanced
  *   KL_DECODE_FUSED_MERGE=0       split sequences merged by a second launch
- * Results are identical under every setting; only the schedule changes.
+ * KL_DECODE_PAIRED and KL_DECODE_FUSED_MERGE leave the output bits unchanged
+ * (except where a full batch's default schedule depends on the fused merge
+ * being available); the other two change how the work is cut or computed,
+ * so outputs agree within the decode tolerance but not bit for bit.
  * Returns KL_OK.
  */
 int kl_paged_decode_reload_options(void);
