@@ -9,7 +9,7 @@ reach the cut's edges: ranges that end inside a charge (a batch of one-page
 sequences beside a long one, so a workgroup's range is shorter than a
 charge), a batch that differs by one page, lengths that differ but not in
 pages (no charge), empty sequences, MQA units (merge kernel), paired KV
-heads, head_dim 32, 64 and 256, pages of 32 and 64 tokens, the FP8 cache
+heads, head_dim 32, 64 and 256, pages of 32, 48, 64 and 256 tokens, the FP8 cache
 and a batch past the scan's 256 sequences. A page the cut dropped or took twice changes the output, so
 each case checks the oracle on up to 8 sequences (the longest among them),
 through the planner and on the balanced schedule, and there the merge kernel
@@ -55,6 +55,8 @@ CASES = [
     ("u5000x24", 32, 8, 128, torch.bfloat16, False, [5], 64),  # 64-token pages: 4 blocks per page
     ("u4000x16", 16, 4, 256, torch.float16, False, [], 32),  # head_dim 256, 32-token pages
     ("u3000x40", 8, 2, 32, torch.bfloat16, False, [1]),  # head_dim 32: the charge at its cap
+    ("u3000x30", 16, 4, 64, torch.bfloat16, False, [2], 48),  # 48-token pages: block -> page by multiply and shift
+    ("u6000x20", 32, 8, 128, torch.float16, False, [], 256),  # 256-token pages: a charge of 2 pages
 ]
 
 
