@@ -26,8 +26,14 @@ extern "C" {
 /* Same handle type as HIP's hipStream_t, declared without including HIP. */
 typedef struct ihipStream_t* kl_stream_t;
 
-/* Element types. Replaces `enum class DType` (csrc/kernel_lab.h:12). */
-typedef enum kl_dtype {
+/* Element types. Replaces `enum class DType` (csrc/kernel_lab.h:12). In C++
+ * the type is int-based, so any int a C caller passes is a value of it and
+ * reaches the library's checks, which reject values outside the list. */
+typedef enum kl_dtype
+#ifdef __cplusplus
+    : int
+#endif
+{
   KL_DTYPE_F32 = 0,
   KL_DTYPE_F16 = 1,
   KL_DTYPE_BF16 = 2

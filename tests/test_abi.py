@@ -239,6 +239,19 @@ def test_requested_splits_normalise_like_the_original(requested, max_pages, want
     assert splits == want
 
 
+@pytest.mark.parametrize("dtype", [-1, 3, 7, 1 << 30])
+def test_out_of_range_dtypes_are_rejected(dtype):
+    """A C caller may pass any int as kl_dtype; the library checks it (the
+    enum is int-based in C++, so such a value is well-defined there too)."""
+    lib = _native.core()
+    splits, ws = ctypes.c_int(-5), ctypes.c_size_t(7)
+    assert lib.kl_paged_decode_plan(dtype, 2, 8, 2, 128, 16, 4, 0, 256, ctypes.byref(splits), ctypes.byref(ws)) == 2
+    assert b"dtype" in lib.kl_last_error()
+    assert lib.kl_rms_norm(dtype, 16, 16, None, 16, 4, 4096, 4096, 1e-6, None) == 2
+    assert lib.kl_paged_decode_attention(dtype, 16, 16, 16, 16, 16, 16, 2, 8, 2, 128, 16, 4, 4, 0.1, 0, None, 0,
+                                         None) == 2
+
+
 def test_planner_rejects_bad_shapes():
     with pytest.raises(ValueError, match="multiple"):
         ops.plan_decode(torch.float16, 2, 3, 2, 128, 16, 4)
