@@ -36,6 +36,8 @@ def capture(fn):
         ([5000, 3, 700, 64], 32, 8, torch.bfloat16, None),  # balanced schedule + merge
         ([900] * 8, 32, 8, torch.float16, 4),  # uniform splits + merge
         ([300, 40], 8, 2, torch.float32, None),  # VALU kernel
+        ([(37 * i) % 6000 + 1 for i in range(64)], 32, 1, torch.bfloat16, None),  # ragged MQA: charged cut, merge kernel
+        ([(53 * i) % 3000 + 1 for i in range(64)], 32, 8, torch.float16, None),  # ragged full batch: pairs, in-kernel merge
     ],
 )
 def test_decode_graph_replays_match_eager(gpu_ops, lens, hq, hkv, dtype, splits):
