@@ -15,7 +15,9 @@ each case checks the oracle on up to 8 sequences (the longest among them),
 through the planner and on the balanced schedule, and there the merge kernel
 against the in-kernel merge, whose unit ranges are computed by different
 code (the merge kernel's list_prefix, the decode kernel's schedule_start),
-bit for bit.
+bit for bit. A seeded sweep of ragged batches of 13-300 sequences (past one
+64-lane scan chunk, and past the 256 the charge applies to) checks the same
+on the requested balanced schedule.
 """
 
 from __future__ import annotations
@@ -24,7 +26,7 @@ import pytest
 import torch
 
 from kernel_lab import _native
-from kernel_lab.kv_cache import quantize_fp8, random_decode_problem
+from kernel_lab.kv_cache import device_decode_problem, quantize_fp8, random_decode_problem
 from oracle import reference as ref
 from tests.conftest import decode_parity
 
@@ -101,3 +103,46 @@ def test_charged_cut(gpu_ops, case, schedule):
             kv.seq_lens[rows].cpu()
         )
     decode_parity(got[rows], want, dtype)
+
+
+def _draw_large(seed: int):
+    """A seeded ragged batch of 13-300 sequences (past one 64-lane scan chunk,
+    some past the 256 the charge applies to), empty sequences included."""
+    import random
+
+    rng = random.Random(1000 + seed)
+    batch = rng.choice([rng.randint(13, 64), rng.randint(65, 256), rng.randint(257, 300)])
+    hq, hkv = rng.choice([(32, 8), (32, 1), (64, 8), (16, 4), (8, 2), (24, 3)])
+    head_dim = rng.choice([64, 128])
+    page = rng.choice([16, 16, 32])
+    dtype = rng.choice([torch.float16, torch.bfloat16])
+    hi = rng.choice([300, 2000, 6000])
+    lens = [rng.randint(1, hi) for _ in range(batch)]
+    if rng.random() < 0.3:  # one long sequence among them
+        lens[rng.randrange(batch)] = rng.randint(hi, 4 * hi)
+    empty = sorted(rng.sample(range(batch), rng.randint(0, 3)))
+    return lens, hq, hkv, head_dim, page, dtype, empty
+
+
+@pytest.mark.parametrize("seed", range(64))
+def test_random_large_batches(gpu_ops, seed):
+    lens, hq, hkv, head_dim, page, dtype, empty = _draw_large(seed)
+    case = f"seed={seed} B={len(lens)} {hq}/{hkv}/{head_dim} page={page} {dtype} empty={empty}"
+    print(case, flush=True)
+    q, kv = device_decode_problem(lens, hq, hkv, head_dim, page, dtype=dtype, seed=seed)
+    kv.seq_lens[empty] = 0
+    run = lambda: gpu_ops.paged_decode_attention(q, kv.k_cache, kv.v_cache, kv.block_table, kv.seq_lens,
+                                                 num_splits=gpu_ops.BALANCED)
+    got = run().cpu()
+    with _native.decode_switches(fused_merge="0"):
+        merged = run().cpu()
+    assert torch.isfinite(got).all(), case
+    assert torch.equal(got, merged), case
+    for b in empty:
+        assert not got[b].any(), case
+    live = [b for b in range(len(lens)) if b not in empty]
+    longest = max(live, key=lambda b: lens[b])
+    rows = sorted({longest, live[0], live[len(live) // 2], live[-1]})
+    want = ref.paged_decode_attention(q[rows].cpu().float(), kv.k_cache.cpu(), kv.v_cache.cpu(),
+                                      kv.block_table[rows].cpu(), kv.seq_lens[rows].cpu())
+    decode_parity(got[rows], want, dtype, case)
