@@ -13,7 +13,7 @@ The decode streams 1.07 GB of KV cache per step, which evicts the 256 MB
 Infinity Cache, so the RMSNorm's 128 MB of inputs come from HBM every step
 too. Outputs are checked against the CPU oracle before anything is timed.
 
-Two live passes of K steps each, after W warm-up steps:
+Four live passes, after W warm-up steps:
 * throughput pass: the K steps back to back with nothing between the kernels,
   timed between two device synchronisations;
 * kernel pass: the same K steps with a HIP event pair on the launch stream
